@@ -1,0 +1,240 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 INT8 group-quant matmul path on one MI355X.
+
+A "step" is the INT8 matmul work of one Llama-3-8B decode token at batch 1 (BASELINE config 2 at
+M=1): for each of the 32 layers the fused QKV (6144x4096), O (4096x4096), fused gate/up
+(28672x4096) and down (4096x14336) projections, then the LM head (128256x4096). All 129 weights
+are distinct random-init INT8 tensors resident in HBM (7.97 GB with scales), so no launch finds its
+weight in the 256 MB Infinity Cache. `value` is algorithmic bytes per step / step time (GB/s).
+
+Also reported: the per-launch GB/s and TFLOP/s of every (projection, M) pair of configs 2 and 3,
+the roofline of the dominant kernel, and the CPU oracle's throughput on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+GS = 64
+HIDDEN, FFN, VOCAB, LAYERS = 4096, 14336, 128256, 32
+PROJ = {"qkv": (6144, HIDDEN), "o": (HIDDEN, HIDDEN), "gate_up": (2 * FFN, HIDDEN),
+        "down": (HIDDEN, FFN)}
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_FP32_PEAK_TFLOPS = 157.3  # dense fp32 matrix peak
+METRIC = "INT8 GEMV HBM GB/s (% of peak) + decode tokens/s, Llama-3-8B shapes, 1 GPU"
+
+
+def load_pkg():
+    name = "llm_steadyinfer_amd"
+    spec = importlib.util.spec_from_file_location(name, REPO / "llm-steadyinfer_amd" / "__init__.py")
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def algo_bytes(M, N, K, gs=GS):
+    """Each operand byte counted once: int8 W, fp32 scales, fp32 x, fp32 y."""
+    return N * K + 4 * (N * K // gs) + 4 * M * K + 4 * M * N
+
+
+def make_q8(torch, N, K, gen, dev):
+    """Random-init INT8 weight: W ~ N(0, 0.02) quantised per 64-group with absmax/127 scales."""
+    q = torch.empty((N, K), dtype=torch.int8, device=dev)
+    s = torch.empty((N * K // GS,), dtype=torch.float32, device=dev)
+    rows = max(1, (1 << 26) // K)
+    for r0 in range(0, N, rows):
+        r1 = min(N, r0 + rows)
+        w = torch.randn((r1 - r0, K), generator=gen, device=dev, dtype=torch.float32) * 0.02
+        g = w.view(r1 - r0, K // GS, GS)
+        sc = g.abs().amax(-1) / 127.0
+        v = g / torch.where(sc == 0, torch.ones_like(sc), sc).unsqueeze(-1)
+        qq = torch.sign(v) * torch.floor(v.abs() + 0.5)
+        q[r0:r1] = qq.clamp_(-127, 127).to(torch.int8).view(r1 - r0, K)
+        s[r0 * K // GS:r1 * K // GS] = sc.reshape(-1)
+    return q, s
+
+
+class Call:
+    """Pre-bound sq8_matmul call (raw pointers) so the host loop adds little per launch."""
+
+    def __init__(self, sq8, x, q, s, y, stream, ws):
+        M, K = x.shape
+        N = q.shape[0]
+        self.fn = sq8.lib().sq8_matmul
+        wsb = sq8.workspace_bytes(M, N, K, GS)
+        ws_ptr, ws_n = ws.get(wsb)
+        self.args = (x.data_ptr(), q.data_ptr(), s.data_ptr(), y.data_ptr(), M, N, K, GS,
+                     ws_ptr or None, ws_n, stream.cuda_stream)
+        self.M, self.N, self.K = M, N, K
+        self.bytes = algo_bytes(M, N, K)
+        self.flops = 2 * M * N * K
+
+    def __call__(self):
+        rc = self.fn(*self.args)
+        if rc != 0:
+            raise RuntimeError(f"sq8_matmul failed with status {rc}")
+
+
+def cpu_baseline(torch, weights, budget_s=10.0):
+    """Oracle CPU loop (reference CPU GEMM structure, OpenMP) on one layer's four projections at
+    M=1, repeated for about budget_s seconds; returns GB/s by the same byte formula."""
+    sys.path.insert(0, str(REPO))
+    import numpy as np
+    from oracle import sq8_oracle as o
+    layer = [(p, weights[p][0][0].cpu().numpy(), weights[p][0][1].cpu().numpy()) for p in PROJ]
+    rng = np.random.default_rng(0)
+    xs = {p: rng.standard_normal((1, PROJ[p][1]), dtype=np.float32) for p in PROJ}
+    for p, q, s in layer:  # warm-up
+        o.matmul_cpu_loop(xs[p], q, s, GS)
+    total_b, reps, t0 = 0, 0, time.perf_counter()
+    while True:
+        for p, q, s in layer:
+            o.matmul_cpu_loop(xs[p], q, s, GS)
+            total_b += algo_bytes(1, *PROJ[p])
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return {"value": round(total_b / el / 1e9, 2), "unit": "GB/s", "cores": o.max_threads(),
+            "kind": "port",
+            "sample": f"oracle sq8o_matmul_cpu_loop, M=1, one Llama-3-8B layer (qkv,o,gate_up,down), "
+                      f"{reps} reps in {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the matmul would shard by output rows / K groups, see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    sq8 = load_pkg()
+    sq8.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    ws = sq8.Workspace(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5678)
+
+    t_init = time.perf_counter()
+    weights = {p: [make_q8(torch, N, K, gen, dev) for _ in range(LAYERS)] for p, (N, K) in PROJ.items()}
+    lm_head = make_q8(torch, VOCAB, HIDDEN, gen, dev)
+    torch.cuda.synchronize()
+    print(f"# weights ready in {time.perf_counter() - t_init:.1f}s", file=sys.stderr, flush=True)
+
+    xgen = torch.Generator(device=dev)
+    xgen.manual_seed(1234)
+
+    def xbuf(M, K):
+        return torch.randn((M, K), generator=xgen, device=dev, dtype=torch.float32)
+
+    # ---------------------------------------------------------------- decode step (M = 1)
+    xin = {p: xbuf(1, K) for p, (N, K) in PROJ.items()}
+    yout = {p: torch.empty((1, N), device=dev) for p, (N, K) in PROJ.items()}
+    calls = []
+    for l in range(LAYERS):
+        for p in PROJ:
+            q, s = weights[p][l]
+            calls.append(Call(sq8, xin[p], q, s, yout[p], stream, ws))
+    x_head, y_head = xbuf(1, HIDDEN), torch.empty((1, VOCAB), device=dev)
+    calls.append(Call(sq8, x_head, lm_head[0], lm_head[1], y_head, stream, ws))
+    step_bytes = sum(c.bytes for c in calls)
+
+    def step():
+        for c in calls:
+            c()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    value = step_bytes / dt / 1e9
+
+    # Per-launch kernel time of the dominant kernel (the M=1 GEMV) with HIP events on the stream
+    # the kernels run on, over further steps.
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in calls]
+    kern_ms, kern_bytes, nlaunch = 0.0, 0, 0
+    for _ in range(3):
+        for c, (a, b) in zip(calls, ev):
+            a.record(stream)
+            c()
+            b.record(stream)
+        torch.cuda.synchronize()
+        kern_ms += sum(a.elapsed_time(b) for a, b in ev)
+        kern_bytes += step_bytes
+        nlaunch += len(calls)
+    achieved = kern_bytes / (kern_ms / 1e3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "sq8 gemv_rows_kernel<8,1,64> (M=1)",
+                "avg_launch_us": round(kern_ms * 1e3 / nlaunch, 2),
+                "algo_bytes_per_launch": round(kern_bytes / nlaunch)}
+
+    # ---------------------------------------------------------------- configs 2 and 3 sweep
+    sweep = []
+    if not args.no_sweep:
+        for M in (1, 8, 32, 64, 2048):
+            for p, (N, K) in PROJ.items():
+                x, y = xbuf(M, K), torch.empty((M, N), device=dev)
+                reps = LAYERS if M <= 64 else 4
+                cs = [Call(sq8, x, *weights[p][l % LAYERS], y, stream, ws) for l in range(reps)]
+                cs[0]()
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                for c in cs:
+                    c()
+                b.record(stream)
+                torch.cuda.synchronize()
+                us = a.elapsed_time(b) * 1e3 / reps
+                sweep.append({"proj": p, "M": M, "N": N, "K": K, "path": sq8.path_name(M, N, K, GS),
+                              "us": round(us, 2), "GB/s": round(cs[0].bytes / us / 1e3, 1),
+                              "TFLOP/s": round(cs[0].flops / us / 1e6, 2)})
+                del x, y, cs
+            print(f"# sweep M={M} done", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(torch, weights, args.cpu_seconds)
+
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8w_f32",
+        "data": "synthetic (random-init N(0,0.02) weights, group-64 absmax INT8; x ~ N(0,1))",
+        "config": {"workload": "Llama-3-8B INT8 decode matmuls, batch 1: 32 x (qkv 6144x4096, "
+                               "o 4096x4096, gate_up 28672x4096, down 4096x14336) + lm_head "
+                               "128256x4096, group 64", "global_batch": 1, "parallelism": "none"},
+        "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        "decode_matmul_tokens_per_s": round(1.0 / dt, 1),
+        "step_algo_bytes": step_bytes,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "sweep": sweep,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,66 @@
+/*
+ * sq8.h - C ABI of the MI355X (gfx950) group-quantised INT8 matmul backend.
+ *
+ * The path: y[m, n] = sum_k x[m, k] * scale(n, k) * (float)w[n, k]
+ *   x      fp32  [M][K]   activations (M tokens, row-major)
+ *   w      int8  [N][K]   symmetric group-quantised weight (row-major, one row per output)
+ *   scales fp32  [N*K/group_size]  per-group scales; scale(n, k) = scales[(n*K)/gs + k/gs]
+ *   y      fp32  [M][N]   output
+ *
+ * This replaces the body of the reference's quantised matmul kernel, whose C++ signature is
+ *   void matmul_kernel_cu_qint8(const Tensor& input, const Tensor& weight, const Tensor& output,
+ *                               int32_t group_size, const Tensor& scale, const CudaConfig* config)
+ * (reference: src/source/op/kernels/cuda/matmul_kernel.cu:162-196, typedef MatmulKernelQuant at
+ *  src/source/op/kernels/kernels_interface.h:12-14, selected by get_matmul_kernel_quant8 at
+ *  src/source/op/kernels/kernels_interfaces.cpp:54-61). The reference names the input width
+ *  "M" and the output rows "K" (matmul.cpp:97-100); this header uses BLAS names: M tokens,
+ *  N outputs, K inputs.
+ *
+ * Conventions:
+ *   - every pointer is a device pointer owned by the caller; nothing is allocated or freed;
+ *   - calls are asynchronous on `hip_stream` (a hipStream_t; NULL = the null stream);
+ *   - errors are returned as negative codes (never abort); 0 is success;
+ *   - the only global state is a per-device cache of the compute-unit count.
+ */
+#ifndef SQ8_H_
+#define SQ8_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum sq8_status {
+  SQ8_OK = 0,
+  SQ8_ERR_NULL = -1,        /* a required pointer is NULL */
+  SQ8_ERR_DIMS = -2,        /* M, N or K <= 0, or K % 4 != 0 (reference CHECK_EQ(M % 4, 0), matmul_kernel.cu:185) */
+  SQ8_ERR_GROUP = -3,       /* group_size <= 0, or N*K not a multiple of group_size (layer.cpp:210) */
+  SQ8_ERR_WORKSPACE = -4,   /* workspace smaller than sq8_workspace_bytes() */
+  SQ8_ERR_LAUNCH = -5,      /* a HIP launch failed; hipGetLastError() holds the cause */
+  SQ8_ERR_DEVICE = -6       /* no usable HIP device */
+};
+
+/* Replaces the launch in matmul_kernel_cu_qint8 (matmul_kernel.cu:186-195): computes y for all
+ * M token rows of x. Shapes and the scale indexing follow the reference kernel exactly
+ * (matmul_kernel.cu:76-88), including group sizes that do not divide K. */
+int sq8_matmul(const float* x, const int8_t* w, const float* scales, float* y, int M, int N, int K,
+               int group_size, void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/* Bytes of device workspace sq8_matmul needs for this shape (0 when none). The reference
+ * kernel needs none (matmul_kernel.cu:65-99); the MFMA paths stage converted activations and
+ * split-K partials here. */
+size_t sq8_workspace_bytes(int M, int N, int K, int group_size);
+
+/* Human-readable text of a status code. */
+const char* sq8_status_string(int status);
+
+/* Name of the kernel family sq8_matmul selects for a shape ("gemv", "mfma_skinny",
+ * "mfma_gemm", "generic"); lets tests and benchmarks check which path ran. */
+const char* sq8_path_name(int M, int N, int K, int group_size);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SQ8_H_ */

@@ -1,0 +1,48 @@
+// Shared device helpers for the gfx950 group-quantised INT8 matmul kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace sq8 {
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));  // 16 int8 weights as one dwordx4
+
+// Launchers (host side). Each returns hipSuccess or the launch error.
+hipError_t launch_gemv(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
+                       int K, int gs, hipStream_t st);
+hipError_t launch_generic(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
+                          int K, int gs, hipStream_t st);
+
+// Sign-extend byte `b` (0..3) of a dword and convert to fp32; exact for int8.
+__device__ __forceinline__ float byte_to_f32(uint32_t d, int b) {
+  return static_cast<float>(static_cast<int32_t>(d << (24 - 8 * b)) >> 24);
+}
+
+// Sum over the 16 int8 of `q` times the 16 fp32 of x[0..3]; the per-group scale is applied by
+// the caller once per 16-element chunk (all 16 lie in one group when group_size % 16 == 0).
+__device__ __forceinline__ float dot16(const i32x4 q, const float4 x0, const float4 x1,
+                                       const float4 x2, const float4 x3) {
+  const uint32_t d0 = static_cast<uint32_t>(q.x), d1 = static_cast<uint32_t>(q.y);
+  const uint32_t d2 = static_cast<uint32_t>(q.z), d3 = static_cast<uint32_t>(q.w);
+  float a = x0.x * byte_to_f32(d0, 0);
+  float b = x0.y * byte_to_f32(d0, 1);
+  a = fmaf(x0.z, byte_to_f32(d0, 2), a);
+  b = fmaf(x0.w, byte_to_f32(d0, 3), b);
+  a = fmaf(x1.x, byte_to_f32(d1, 0), a);
+  b = fmaf(x1.y, byte_to_f32(d1, 1), b);
+  a = fmaf(x1.z, byte_to_f32(d1, 2), a);
+  b = fmaf(x1.w, byte_to_f32(d1, 3), b);
+  a = fmaf(x2.x, byte_to_f32(d2, 0), a);
+  b = fmaf(x2.y, byte_to_f32(d2, 1), b);
+  a = fmaf(x2.z, byte_to_f32(d2, 2), a);
+  b = fmaf(x2.w, byte_to_f32(d2, 3), b);
+  a = fmaf(x3.x, byte_to_f32(d3, 0), a);
+  b = fmaf(x3.y, byte_to_f32(d3, 1), b);
+  a = fmaf(x3.z, byte_to_f32(d3, 2), a);
+  b = fmaf(x3.w, byte_to_f32(d3, 3), b);
+  return a + b;
+}
+
+}  // namespace sq8

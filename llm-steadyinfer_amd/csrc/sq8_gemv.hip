@@ -1,0 +1,193 @@
+// Bandwidth-bound decode kernels (few token rows) for gfx950.
+//
+// Reference behaviour replaced: matmul_kernel_cu_fp32int8<128> (matmul_kernel.cu:65-99), one
+// 128-thread block per output row with 1-byte scalar weight loads, a per-element scale gather and
+// a cub block reduction per (row, token).
+//
+// Design here: a 256-thread workgroup (4 wave64s) owns R consecutive output rows and the whole K
+// extent. Every lane streams 16 int8 weights per row per step with one dwordx4 load; the 256 lanes
+// of a workgroup cover 4 KiB of each row per step, fully coalesced. A 16-byte chunk never straddles
+// a K-group (group_size % 16 == 0), so the lane applies its group scale once per chunk after a
+// 16-term fp32 dot product. The R x MT partial sums of a lane are reduced across the wave with a
+// reduce-scatter butterfly (R*MT values in log2(R*MT) exchange rounds instead of 6 rounds each),
+// then across the 4 waves through LDS in a fixed order, so results are deterministic.
+#include "sq8_common.h"
+
+namespace sq8 {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+
+// Reduce NV per-lane values over the 64 lanes of a wave. On return v[0] of lane l holds the
+// wave-wide sum of value index (l >> (6 - log2 NV)). Every value is summed in the same pairing
+// order (xor 32, 16, 8, 4, 2, 1) whatever NV is, so the result of a (row, token) pair does not
+// depend on how many tokens share the launch.
+template <int NV>
+__device__ __forceinline__ void wave_reduce_scatter(float (&v)[NV], int lane) {
+  static_assert((NV & (NV - 1)) == 0 && NV <= 64, "NV must be a power of two <= 64");
+  int off = 32;
+#pragma unroll
+  for (int half = NV / 2; half >= 1; half /= 2, off /= 2) {
+    const bool upper = (lane & off) != 0;
+#pragma unroll
+    for (int i = 0; i < half; ++i) {
+      const float send = upper ? v[i] : v[i + half];
+      const float keep = upper ? v[i + half] : v[i];
+      v[i] = keep + __shfl_xor(send, off, kWave);
+    }
+  }
+#pragma unroll
+  for (; off >= 1; off /= 2) v[0] += __shfl_xor(v[0], off, kWave);
+}
+
+// R rows per workgroup, MT token rows per pass, GS = group size (0: runtime value, multiple of 16).
+template <int R, int MT, int GS>
+__global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const float* __restrict__ x,
+                                                             const int8_t* __restrict__ w,
+                                                             const float* __restrict__ s,
+                                                             float* __restrict__ y, int M, int N,
+                                                             int K, int gs_rt) {
+  constexpr int NV = R * MT;
+  __shared__ float red[kWaves][NV];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int n0 = blockIdx.x * R;
+  const int gs = GS ? GS : gs_rt;
+  const int chunks_per_group = gs >> 4;
+  const int nchunk = K >> 4;
+  const int groups_per_row = K / gs;
+
+  // Rows past N are clamped to the last row (loads stay in bounds); their sums are not stored.
+  const i32x4* wrow[R];
+  const float* srow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int n = min(n0 + r, N - 1);
+    wrow[r] = reinterpret_cast<const i32x4*>(w + static_cast<size_t>(n) * K);
+    srow[r] = s + static_cast<size_t>(n) * groups_per_row;
+  }
+
+  for (int m0 = 0; m0 < M; m0 += MT) {
+    const float4* xrow[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int m = min(m0 + t, M - 1);
+      xrow[t] = reinterpret_cast<const float4*>(x + static_cast<size_t>(m) * K);
+    }
+    float acc[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) acc[i] = 0.f;
+
+#pragma unroll 2
+    for (int c = tid; c < nchunk; c += kThreads) {
+      const int g = GS ? (c / ((GS > 0 ? GS : 16) / 16)) : (c / chunks_per_group);
+      i32x4 q[R];
+      float sc[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        q[r] = __builtin_nontemporal_load(wrow[r] + c);
+        sc[r] = srow[r][g];
+      }
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const float4 x0 = xrow[t][4 * c + 0];
+        const float4 x1 = xrow[t][4 * c + 1];
+        const float4 x2 = xrow[t][4 * c + 2];
+        const float4 x3 = xrow[t][4 * c + 3];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          acc[r * MT + t] = fmaf(sc[r], dot16(q[r], x0, x1, x2, x3), acc[r * MT + t]);
+        }
+      }
+    }
+
+    wave_reduce_scatter<NV>(acc, lane);
+    constexpr int kSpan = kWave / NV;  // lanes that end up holding the same value index
+    if ((lane & (kSpan - 1)) == 0) red[wave][lane / kSpan] = acc[0];
+    __syncthreads();
+    if (tid < NV) {
+      const int r = tid / MT, t = tid % MT;
+      float v = red[0][tid];
+#pragma unroll
+      for (int wv = 1; wv < kWaves; ++wv) v += red[wv][tid];
+      const int n = n0 + r, m = m0 + t;
+      if (n < N && m < M) y[static_cast<size_t>(m) * N + n] = v;
+    }
+    __syncthreads();
+  }
+}
+
+// Exact restatement of the reference indexing for any group size and any K % 4 == 0, used when
+// the fast path's alignment or group-size assumptions do not hold: scale of (n, k) is
+// scales[(n*K)/gs + k/gs] (matmul_kernel.cu:77,86). One workgroup per (row, token).
+__global__ __launch_bounds__(kThreads) void generic_kernel(const float* __restrict__ x,
+                                                          const int8_t* __restrict__ w,
+                                                          const float* __restrict__ s,
+                                                          float* __restrict__ y, int M, int N,
+                                                          int K, int gs) {
+  __shared__ float red[kWaves];
+  const int n = blockIdx.x;
+  const int m = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int8_t* wr = w + static_cast<size_t>(n) * K;
+  const float* sr = s + (static_cast<int64_t>(n) * K) / gs;
+  const float* xr = x + static_cast<size_t>(m) * K;
+  float acc = 0.f;
+  for (int k = tid; k < K; k += kThreads) {
+    acc = fmaf(xr[k] * sr[k / gs], static_cast<float>(wr[k]), acc);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off /= 2) acc += __shfl_xor(acc, off, kWave);
+  if ((tid & (kWave - 1)) == 0) red[tid >> 6] = acc;
+  __syncthreads();
+  if (tid == 0) {
+    float v = red[0];
+#pragma unroll
+    for (int wv = 1; wv < kWaves; ++wv) v += red[wv];
+    y[static_cast<size_t>(m) * N + n] = v;
+  }
+}
+
+template <int R, int MT>
+hipError_t launch_rows(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
+                       int K, int gs, hipStream_t st) {
+  const dim3 grid((N + R - 1) / R);
+  if (gs == 64) {
+    hipLaunchKernelGGL((gemv_rows_kernel<R, MT, 64>), grid, dim3(kThreads), 0, st, x, w, s, y, M,
+                       N, K, gs);
+  } else {
+    hipLaunchKernelGGL((gemv_rows_kernel<R, MT, 0>), grid, dim3(kThreads), 0, st, x, w, s, y, M,
+                       N, K, gs);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// Requires: group_size % 16 == 0, K % group_size == 0, 16-byte aligned x and w.
+hipError_t launch_gemv(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
+                       int K, int gs, hipStream_t st) {
+  if (M == 1) return launch_rows<8, 1>(x, w, s, y, M, N, K, gs, st);
+  if (M == 2) return launch_rows<8, 2>(x, w, s, y, M, N, K, gs, st);
+  return launch_rows<8, 4>(x, w, s, y, M, N, K, gs, st);
+}
+
+hipError_t launch_generic(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
+                          int K, int gs, hipStream_t st) {
+  // One workgroup per (row, token); grid.y is limited to 65535 token rows per launch.
+  for (int m0 = 0; m0 < M; m0 += 65535) {
+    const int mc = min(M - m0, 65535);
+    hipLaunchKernelGGL(generic_kernel, dim3(N, mc), dim3(kThreads), 0, st,
+                       x + static_cast<size_t>(m0) * K, w, s, y + static_cast<size_t>(m0) * N,
+                       mc, N, K, gs);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+}  // namespace sq8
