@@ -10,16 +10,19 @@ namespace {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-enum class Path { kGemv, kGeneric };
+enum class Path { kGemv, kMfma, kGeneric };
 
 // Fast kernels need 16-element chunks that never straddle a group and rows that start on a
 // group boundary; everything else goes to the exact generic kernel.
 bool fast_shape(int K, int gs) { return gs % 16 == 0 && K % gs == 0; }
 
+// Token rows at which the matrix-core path takes over from the VALU GEMV.
+constexpr int kMfmaMinM = 3;
+
 Path choose(int M, int N, int K, int gs, bool aligned) {
-  (void)M;
   (void)N;
   if (!aligned || !fast_shape(K, gs)) return Path::kGeneric;
+  if (M >= kMfmaMinM && gs % 64 == 0) return Path::kMfma;
   return Path::kGemv;
 }
 
@@ -39,14 +42,17 @@ int sq8_matmul(const float* x, const int8_t* w, const float* scales, float* y, i
                int group_size, void* workspace, size_t workspace_bytes, void* hip_stream) {
   const int v = validate(x, w, scales, y, M, N, K, group_size);
   if (v != SQ8_OK) return v;
-  if (workspace_bytes < sq8_workspace_bytes(M, N, K, group_size)) return SQ8_ERR_WORKSPACE;
-  (void)workspace;
+  const size_t need = sq8_workspace_bytes(M, N, K, group_size);
+  if (workspace_bytes < need || (need > 0 && workspace == nullptr)) return SQ8_ERR_WORKSPACE;
   hipStream_t st = static_cast<hipStream_t>(hip_stream);
   const bool aligned = aligned16(x) && aligned16(w);
   hipError_t e = hipSuccess;
   switch (choose(M, N, K, group_size, aligned)) {
     case Path::kGemv:
       e = sq8::launch_gemv(x, w, scales, y, M, N, K, group_size, st);
+      break;
+    case Path::kMfma:
+      e = sq8::launch_mfma(x, w, scales, y, M, N, K, group_size, workspace, st);
       break;
     case Path::kGeneric:
       e = sq8::launch_generic(x, w, scales, y, M, N, K, group_size, st);
@@ -56,11 +62,9 @@ int sq8_matmul(const float* x, const int8_t* w, const float* scales, float* y, i
 }
 
 size_t sq8_workspace_bytes(int M, int N, int K, int group_size) {
-  (void)M;
-  (void)N;
-  (void)K;
-  (void)group_size;
-  return 0;
+  if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0) return 0;
+  if (choose(M, N, K, group_size, true) != Path::kMfma) return 0;
+  return sq8::mfma_workspace_bytes(M, N, K);
 }
 
 const char* sq8_status_string(int status) {
@@ -80,6 +84,7 @@ const char* sq8_path_name(int M, int N, int K, int group_size) {
   if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0) return "invalid";
   switch (choose(M, N, K, group_size, true)) {
     case Path::kGemv: return "gemv";
+    case Path::kMfma: return "mfma";
     case Path::kGeneric: return "generic";
   }
   return "invalid";

@@ -12,6 +12,11 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));  // 16 int8 weights as on
 // Launchers (host side). Each returns hipSuccess or the launch error.
 hipError_t launch_gemv(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
                        int K, int gs, hipStream_t st);
+int cu_count();
+size_t mfma_workspace_bytes(int M, int N, int K);
+hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
+                       int K, int gs, void* ws, hipStream_t st);
+bool gemv_stream_fits(int M, int K);
 hipError_t launch_generic(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
                           int K, int gs, hipStream_t st);
 

@@ -4,7 +4,14 @@
 // 128-thread block per output row with 1-byte scalar weight loads, a per-element scale gather and
 // a cub block reduction per (row, token).
 //
-// Design here: a 256-thread workgroup (4 wave64s) owns R consecutive output rows and the whole K
+// Two kernels:
+//  - stream_kernel (M <= 2, the decode GEMV): persistent waves; each wave owns blocks of R output
+//    rows and streams them in steps of U KiB per row, with the next step's weight loads issued
+//    before the current step is consumed (two register sets), so a wave always has loads in flight.
+//    The token rows are staged once per workgroup in LDS. Each lane converts its 16 int8 per row
+//    with SDWA byte-select conversions and applies the group scale once per 16-element chunk.
+//  - gemv_rows_kernel (fallback for larger M or K beyond the LDS budget):
+// a 256-thread workgroup (4 wave64s) owns R consecutive output rows and the whole K
 // extent. Every lane streams 16 int8 weights per row per step with one dwordx4 load; the 256 lanes
 // of a workgroup cover 4 KiB of each row per step, fully coalesced. A 16-byte chunk never straddles
 // a K-group (group_size % 16 == 0), so the lane applies its group scale once per chunk after a
@@ -121,6 +128,96 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const float* __rest
   }
 }
 
+// Persistent decode GEMV. MT token rows (MT = M <= 2) are staged in LDS; wave w of the grid owns
+// row blocks w, w + GW, ... of R rows. A step is U iterations of 1 KiB per row (64 lanes x 16 B).
+template <int R, int U, int MT, int GS>
+__global__ __launch_bounds__(kThreads) void stream_kernel(const float* __restrict__ x,
+                                                          const int8_t* __restrict__ w,
+                                                          const float* __restrict__ s,
+                                                          float* __restrict__ y, int N, int K,
+                                                          int gs_rt) {
+  extern __shared__ float xs[];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int nblk = (N + R - 1) / R;
+  const int GW = gridDim.x * kWaves;
+  const int gw = blockIdx.x * kWaves + wave;
+  const int its = (K + 1023) >> 10;
+  const int nsteps = (its + U - 1) / U;  // steps per row block
+  const int gs = GS ? GS : gs_rt;
+  const int gpr = K / gs;
+
+  i32x4 qa[U][R], qb[U][R];
+  float sa[U][R], sb[U][R];
+  auto load = [&](int b, int st, i32x4 (&q)[U][R], float (&sc)[U][R]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = (st * U + u) * 1024 + lane * 16;
+      const bool ok = k < K;
+      const int kc = ok ? k : 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int n = min(b * R + r, N - 1);
+        const i32x4 v =
+            __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(w + static_cast<size_t>(n) * K + kc));
+        q[u][r] = ok ? v : i32x4{0, 0, 0, 0};
+        sc[u][r] = s[static_cast<size_t>(n) * gpr + kc / gs];
+      }
+    }
+  };
+  float acc[R * MT];
+#pragma unroll
+  for (int i = 0; i < R * MT; ++i) acc[i] = 0.f;
+  auto consume = [&](int b, int st, const i32x4 (&q)[U][R], const float (&sc)[U][R]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = (st * U + u) * 1024 + lane * 16;
+      const int kc = k < K ? k : 0;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const float4* xp = reinterpret_cast<const float4*>(xs + t * K + kc);
+        const float4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          acc[r * MT + t] = fmaf(sc[u][r], dot16(q[u][r], x0, x1, x2, x3), acc[r * MT + t]);
+      }
+    }
+    if (st == nsteps - 1) {
+      wave_reduce_scatter<R * MT>(acc, lane);
+      constexpr int kSpan = kWave / (R * MT);
+      if ((lane & (kSpan - 1)) == 0) {
+        const int idx = lane / kSpan, r = idx / MT, t = idx % MT;
+        const int n = b * R + r;
+        if (n < N) y[static_cast<size_t>(t) * N + n] = acc[0];
+      }
+#pragma unroll
+      for (int i = 0; i < R * MT; ++i) acc[i] = 0.f;
+    }
+  };
+
+  int b = gw, st = 0;
+  if (b < nblk) load(b, st, qa, sa);
+  // Stage x after the first weight loads are in flight.
+  for (int i = tid * 4; i < MT * K; i += kThreads * 4)
+    *reinterpret_cast<float4*>(xs + i) = *reinterpret_cast<const float4*>(x + i);
+  __syncthreads();
+  while (b < nblk) {
+    int b1 = b, st1 = st + 1;
+    if (st1 == nsteps) { st1 = 0; b1 += GW; }
+    if (b1 < nblk) load(b1, st1, qb, sb);
+    consume(b, st, qa, sa);
+    b = b1;
+    st = st1;
+    if (b >= nblk) break;
+    b1 = b;
+    st1 = st + 1;
+    if (st1 == nsteps) { st1 = 0; b1 += GW; }
+    if (b1 < nblk) load(b1, st1, qa, sa);
+    consume(b, st, qb, sb);
+    b = b1;
+    st = st1;
+  }
+}
+
 // Exact restatement of the reference indexing for any group size and any K % 4 == 0, used when
 // the fast path's alignment or group-size assumptions do not hold: scale of (n, k) is
 // scales[(n*K)/gs + k/gs] (matmul_kernel.cu:77,86). One workgroup per (row, token).
@@ -168,9 +265,63 @@ hipError_t launch_rows(const float* x, const int8_t* w, const float* s, float* y
 
 }  // namespace
 
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+namespace {
+
+// LDS bytes the stream kernel may use for staged token rows (MT * K fp32).
+constexpr size_t kStreamLdsMax = 64 * 1024;
+
+template <int R, int U, int MT, int GS>
+hipError_t launch_stream_t(const float* x, const int8_t* w, const float* s, float* y, int N, int K,
+                           int gs, hipStream_t st) {
+  auto kern = stream_kernel<R, U, MT, GS>;
+  const size_t lds = static_cast<size_t>(MT) * K * sizeof(float);
+  // Resident workgroups per CU for this kernel: its register use allows 7-8; 8 is enough to keep
+  // two steps of loads in flight per wave.
+  constexpr int kWgPerCu = 8;
+  const int nblk = (N + R - 1) / R;
+  const int grid = min((nblk + kWaves - 1) / kWaves, cu_count() * kWgPerCu);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, st, x, w, s, y, N, K, gs);
+  return hipGetLastError();
+}
+
+template <int MT>
+hipError_t launch_stream(const float* x, const int8_t* w, const float* s, float* y, int N, int K,
+                         int gs, hipStream_t st) {
+  // Long rows (K >= 8 KiB): two 1 KiB iterations per step; short rows: four.
+  if (K >= 8192) {
+    return gs == 64 ? launch_stream_t<2, 2, MT, 64>(x, w, s, y, N, K, gs, st)
+                    : launch_stream_t<2, 2, MT, 0>(x, w, s, y, N, K, gs, st);
+  }
+  return gs == 64 ? launch_stream_t<2, 4, MT, 64>(x, w, s, y, N, K, gs, st)
+                  : launch_stream_t<2, 4, MT, 0>(x, w, s, y, N, K, gs, st);
+}
+
+}  // namespace
+
+bool gemv_stream_fits(int M, int K) {
+  return M <= 2 && static_cast<size_t>(M) * K * sizeof(float) <= kStreamLdsMax;
+}
+
 // Requires: group_size % 16 == 0, K % group_size == 0, 16-byte aligned x and w.
 hipError_t launch_gemv(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
                        int K, int gs, hipStream_t st) {
+  if (gemv_stream_fits(M, K)) {
+    return M == 1 ? launch_stream<1>(x, w, s, y, N, K, gs, st)
+                  : launch_stream<2>(x, w, s, y, N, K, gs, st);
+  }
   if (M == 1) return launch_rows<8, 1>(x, w, s, y, M, N, K, gs, st);
   if (M == 2) return launch_rows<8, 2>(x, w, s, y, M, N, K, gs, st);
   return launch_rows<8, 4>(x, w, s, y, M, N, K, gs, st);

@@ -1,0 +1,371 @@
+// MFMA kernels for token counts above the GEMV range (small-batch decode and prefill), gfx950.
+//
+// Reference behaviour replaced: matmul_kernel_cu_fp32int8<128> (matmul_kernel.cu:65-99) computes
+// y[b, n] = sum_k x[b, k] * scale * (float)w[n, k] with fp32 CUDA-core arithmetic, re-reading each
+// weight row once per batch row. Here the product runs on the matrix cores:
+//
+//  * Activations: fp32 cannot feed an f16 MFMA exactly, so each token row is split once into
+//    x * 2^e = hi + lo with hi = f16(x * 2^e) and lo = f16(x * 2^e - hi). The power of two 2^e puts
+//    the row's absmax in [2^13, 2^14), far from f16 overflow, and makes hi + lo carry ~22 bits,
+//    about fp32's precision (split_x_kernel). The output is multiplied back by 2^-e exactly.
+//  * Weights: int8 is exact in f16. A 16-byte chunk is biased to unsigned (xor 0x80), interleaved
+//    with the f16 exponent byte 0x64 by v_perm (giving 1024 + 128 + q), and one packed f16 add of
+//    -1152 yields q exactly: two VALU ops per 4 weights.
+//  * One K step of the main loop is one 64-wide weight group. Its partial product P (hi and lo
+//    MFMAs chained in fp32) is formed from zero, then acc += scale[n, g] * P with one FMA per
+//    output: the per-group scale never touches the weights, so no rounding is added on that side.
+//  * v_mfma_f32_32x32x16_f16 tiles; a 256-thread workgroup (4 waves) owns a BM x BN output tile;
+//    the next group's activations and weights are loaded into registers while the current group is
+//    multiplied from LDS (double-buffered LDS, one barrier per group).
+//  * Skinny shapes (few tokens, few output tiles) split K over gridDim.z; partial tiles go to the
+//    workspace and a second kernel sums them in split order (deterministic).
+#include <algorithm>
+
+#include "sq8_common.h"
+
+namespace sq8 {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int BK = 64;          // K per main-loop step = one weight group of 64
+constexpr int LDS_STRIDE = 72;  // halves per staged row (64 + 8 padding against bank conflicts)
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- activation split
+// One workgroup per token row: absmax, exponent, then hi/lo halves.
+__global__ __launch_bounds__(kThreads) void split_x_kernel(const float* __restrict__ x,
+                                                          _Float16* __restrict__ xh,
+                                                          _Float16* __restrict__ xl,
+                                                          float* __restrict__ rscale, int K) {
+  __shared__ float red[kThreads / kWave];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const float* xr = x + static_cast<size_t>(m) * K;
+  float amax = 0.f;
+  for (int k = tid * 4; k < K; k += kThreads * 4) {
+    const float4 v = *reinterpret_cast<const float4*>(xr + k);
+    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off /= 2) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+  if ((tid & (kWave - 1)) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = 0;
+  if (amax > 0.f && amax <= 3.402823466e38f) {
+    int ex;
+    frexpf(amax, &ex);           // amax = f * 2^ex, f in [0.5, 1)
+    e = min(max(14 - ex, -126), 126);
+  }
+  if (tid == 0) rscale[m] = ldexpf(1.f, -e);
+  _Float16* hr = xh + static_cast<size_t>(m) * K;
+  _Float16* lr = xl + static_cast<size_t>(m) * K;
+  for (int k = tid * 4; k < K; k += kThreads * 4) {
+    const float4 v = *reinterpret_cast<const float4*>(xr + k);
+    const float a[4] = {ldexpf(v.x, e), ldexpf(v.y, e), ldexpf(v.z, e), ldexpf(v.w, e)};
+    _Float16 h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h[i] = static_cast<_Float16>(a[i]);
+      l[i] = static_cast<_Float16>(a[i] - static_cast<float>(h[i]));
+    }
+    *reinterpret_cast<uint2*>(hr + k) = *reinterpret_cast<const uint2*>(h);
+    *reinterpret_cast<uint2*>(lr + k) = *reinterpret_cast<const uint2*>(l);
+  }
+}
+
+// 4 int8 (one dword) -> 4 exact f16 (two dwords), see file comment.
+__device__ __forceinline__ void i8x4_to_h4(uint32_t d, uint32_t& lo, uint32_t& hi) {
+  const uint32_t u = d ^ 0x80808080u;
+  const uint32_t a = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+  const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+  const h2 bias = {static_cast<_Float16>(-1152.f), static_cast<_Float16>(-1152.f)};
+  h2 ha = __builtin_bit_cast(h2, a) + bias;
+  h2 hb = __builtin_bit_cast(h2, b) + bias;
+  lo = __builtin_bit_cast(uint32_t, ha);
+  hi = __builtin_bit_cast(uint32_t, hb);
+}
+
+// ---------------------------------------------------------------- main GEMM
+// Waves laid out WAVES_M x WAVES_N; each wave owns TM x TN tiles of 32 x 32.
+template <int WAVES_M, int WAVES_N, int TM, int TN>
+struct Tile {
+  static_assert(WAVES_M * WAVES_N == kThreads / kWave, "4 waves per workgroup");
+  static constexpr int BM = WAVES_M * TM * 32;
+  static constexpr int BN = WAVES_N * TN * 32;
+  static constexpr int XCH = BM * 8 / kThreads;   // 16-byte x chunks per thread per stage (hi or lo)
+  static constexpr int WCH = BN * 4 / kThreads;   // 16-byte weight chunks per thread per stage
+  static_assert(XCH >= 1 && WCH >= 1, "tile too small for the staging pattern");
+  static constexpr int STAGE_HALVES = (2 * BM + BN) * LDS_STRIDE;
+  static constexpr size_t LDS_BYTES = 2ull * STAGE_HALVES * sizeof(_Float16);
+};
+
+template <int WAVES_M, int WAVES_N, int TM, int TN>
+__global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
+    const _Float16* __restrict__ xh, const _Float16* __restrict__ xl,
+    const float* __restrict__ rscale, const int8_t* __restrict__ w, const float* __restrict__ s,
+    float* __restrict__ out, int M, int N, int K, int gs, int groups_per_split) {
+  using T = Tile<WAVES_M, WAVES_N, TM, TN>;
+  extern __shared__ _Float16 lds[];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int n0 = blockIdx.x * T::BN, m0 = blockIdx.y * T::BM;
+  const int nsteps = K / BK;
+  const int st_begin = blockIdx.z * groups_per_split;
+  const int st_end = min(nsteps, st_begin + groups_per_split);
+  const int gpr = K / gs;
+
+  // Staging assignment (fixed per thread).
+  const _Float16* xh_src[T::XCH];
+  const _Float16* xl_src[T::XCH];
+  int x_dst[T::XCH];
+#pragma unroll
+  for (int i = 0; i < T::XCH; ++i) {
+    const int c = tid + kThreads * i, row = c >> 3, part = c & 7;
+    const int m = min(m0 + row, M - 1);
+    xh_src[i] = xh + static_cast<size_t>(m) * K + part * 8;
+    xl_src[i] = xl + static_cast<size_t>(m) * K + part * 8;
+    x_dst[i] = row * LDS_STRIDE + part * 8;
+  }
+  const int8_t* w_src[T::WCH];
+  int w_dst[T::WCH];
+#pragma unroll
+  for (int i = 0; i < T::WCH; ++i) {
+    const int c = tid + kThreads * i, row = c >> 2, part = c & 3;
+    const int n = min(n0 + row, N - 1);
+    w_src[i] = w + static_cast<size_t>(n) * K + part * 16;
+    w_dst[i] = row * LDS_STRIDE + part * 16;
+  }
+  // Scale pointers for this lane's output columns.
+  const float* s_src[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = min(n0 + (wn * TN + j) * 32 + (lane & 31), N - 1);
+    s_src[j] = s + static_cast<size_t>(n) * gpr;
+  }
+
+  u32x4 rxh[T::XCH], rxl[T::XCH], rw[T::WCH];
+  float rs[TN];
+  auto gload = [&](int st) {
+    const int k0 = st * BK;
+#pragma unroll
+    for (int i = 0; i < T::XCH; ++i) {
+      rxh[i] = *reinterpret_cast<const u32x4*>(xh_src[i] + k0);
+      rxl[i] = *reinterpret_cast<const u32x4*>(xl_src[i] + k0);
+    }
+#pragma unroll
+    for (int i = 0; i < T::WCH; ++i)
+      rw[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w_src[i] + k0));
+#pragma unroll
+    for (int j = 0; j < TN; ++j) rs[j] = s_src[j][k0 / gs];
+  };
+  auto lstore = [&](int buf) {
+    _Float16* sxh = lds + buf * T::STAGE_HALVES;
+    _Float16* sxl = sxh + T::BM * LDS_STRIDE;
+    _Float16* sw = sxl + T::BM * LDS_STRIDE;
+#pragma unroll
+    for (int i = 0; i < T::XCH; ++i) {
+      *reinterpret_cast<u32x4*>(sxh + x_dst[i]) = rxh[i];
+      *reinterpret_cast<u32x4*>(sxl + x_dst[i]) = rxl[i];
+    }
+#pragma unroll
+    for (int i = 0; i < T::WCH; ++i) {
+      uint32_t h[8];
+      i8x4_to_h4(rw[i].x, h[0], h[1]);
+      i8x4_to_h4(rw[i].y, h[2], h[3]);
+      i8x4_to_h4(rw[i].z, h[4], h[5]);
+      i8x4_to_h4(rw[i].w, h[6], h[7]);
+      const u32x4 a = {h[0], h[1], h[2], h[3]};
+      const u32x4 b = {h[4], h[5], h[6], h[7]};
+      *reinterpret_cast<u32x4*>(sw + w_dst[i]) = a;
+      *reinterpret_cast<u32x4*>(sw + w_dst[i] + 8) = b;
+    }
+  };
+
+  f16v acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // Lane's operand rows/columns inside the stage and its 32-wide K half.
+  const int lrow = lane & 31, khalf = (lane >> 5) * 32;
+  float cur_s[TN];
+  if (st_begin < st_end) {
+    gload(st_begin);
+    lstore(0);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) cur_s[j] = rs[j];
+  }
+  __syncthreads();
+  for (int st = st_begin; st < st_end; ++st) {
+    const int buf = (st - st_begin) & 1;
+    const bool more = st + 1 < st_end;
+    if (more) gload(st + 1);
+    const _Float16* sxh = lds + buf * T::STAGE_HALVES;
+    const _Float16* sxl = sxh + T::BM * LDS_STRIDE;
+    const _Float16* sw = sxl + T::BM * LDS_STRIDE;
+    f16v p[TM][TN];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int ko = khalf + 8 * t;
+      h8 ah[TM], al[TM], bw[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = (wm * TM + i) * 32 + lrow;
+        ah[i] = *reinterpret_cast<const h8*>(sxh + row * LDS_STRIDE + ko);
+        al[i] = *reinterpret_cast<const h8*>(sxl + row * LDS_STRIDE + ko);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int col = (wn * TN + j) * 32 + lrow;
+        bw[j] = *reinterpret_cast<const h8*>(sw + col * LDS_STRIDE + ko);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          if (t == 0) {
+            const f16v zero = {};
+            p[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j], zero, 0, 0, 0);
+          } else {
+            p[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j], p[i][j], 0, 0, 0);
+          }
+          p[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bw[j], p[i][j], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(cur_s[j], p[i][j][r], acc[i][j][r]);
+    if (more) {
+      lstore(buf ^ 1);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) cur_s[j] = rs[j];
+    }
+    __syncthreads();
+  }
+
+  // Epilogue: undo the activation power of two and store (to y, or to this split's partial).
+  float* dst = out + static_cast<size_t>(blockIdx.z) * M * N;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + (wm * TM + i) * 32 + 8 * (r >> 2) + (lane >> 5) * 4 + (r & 3);
+      if (m >= M) continue;
+      const float rsc = rscale[m];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + (wn * TN + j) * 32 + lrow;
+        if (n < N) dst[static_cast<size_t>(m) * N + n] = acc[i][j][r] * rsc;
+      }
+    }
+  }
+}
+
+// Sum split-K partials in split order: y[i] = sum_z part[z][i].
+__global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(const float* __restrict__ part,
+                                                                float* __restrict__ y,
+                                                                size_t count, int splits) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x; i < count;
+       i += static_cast<size_t>(gridDim.x) * kThreads) {
+    float v = part[i];
+    for (int z = 1; z < splits; ++z) v += part[static_cast<size_t>(z) * count + i];
+    y[i] = v;
+  }
+}
+
+size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+struct Plan {
+  int cfg;        // 0: 32x256 tile, 1: 64x128, 2: 128x128
+  int bm, bn;
+  int splits;
+  int groups_per_split;
+};
+
+Plan make_plan(int M, int N, int K) {
+  Plan p{};
+  if (M <= 32) { p.cfg = 0; p.bm = 32; p.bn = 256; }
+  else if (M <= 64) { p.cfg = 1; p.bm = 64; p.bn = 128; }
+  else { p.cfg = 2; p.bm = 128; p.bn = 128; }
+  const int tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
+  const int nsteps = K / BK;
+  const int target = 2 * cu_count();
+  int splits = 1;
+  if (tiles < target) splits = min(min(16, nsteps), (target + tiles - 1) / tiles);
+  p.groups_per_split = (nsteps + splits - 1) / splits;
+  p.splits = (nsteps + p.groups_per_split - 1) / p.groups_per_split;
+  return p;
+}
+
+template <int WM, int WN, int TM, int TN>
+hipError_t launch_gemm(const _Float16* xh, const _Float16* xl, const float* rsc, const int8_t* w,
+                       const float* s, float* out, int M, int N, int K, int gs, const Plan& p,
+                       hipStream_t st) {
+  using T = Tile<WM, WN, TM, TN>;
+  auto kern = mfma_gemm_kernel<WM, WN, TM, TN>;
+  static bool attr_set = false;  // LDS above 64 KiB needs the opt-in attribute
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(T::LDS_BYTES));
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const dim3 grid((N + T::BN - 1) / T::BN, (M + T::BM - 1) / T::BM, p.splits);
+  hipLaunchKernelGGL(kern, grid, dim3(kThreads), T::LDS_BYTES, st, xh, xl, rsc, w, s, out, M, N, K,
+                     gs, p.groups_per_split);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t mfma_workspace_bytes(int M, int N, int K) {
+  const Plan p = make_plan(M, N, K);
+  size_t b = 2 * align256(static_cast<size_t>(M) * K * sizeof(_Float16));
+  b += align256(static_cast<size_t>(M) * sizeof(float));
+  if (p.splits > 1) b += align256(static_cast<size_t>(p.splits) * M * N * sizeof(float));
+  return b;
+}
+
+// Requires: K % 64 == 0, group_size % 64 == 0, K % group_size == 0, 16-byte aligned x and w,
+// workspace of mfma_workspace_bytes(M, N, K).
+hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
+                       int K, int gs, void* ws, hipStream_t st) {
+  const Plan p = make_plan(M, N, K);
+  char* base = static_cast<char*>(ws);
+  _Float16* xh = reinterpret_cast<_Float16*>(base);
+  base += align256(static_cast<size_t>(M) * K * sizeof(_Float16));
+  _Float16* xl = reinterpret_cast<_Float16*>(base);
+  base += align256(static_cast<size_t>(M) * K * sizeof(_Float16));
+  float* rsc = reinterpret_cast<float*>(base);
+  base += align256(static_cast<size_t>(M) * sizeof(float));
+  float* part = p.splits > 1 ? reinterpret_cast<float*>(base) : y;
+
+  hipLaunchKernelGGL(split_x_kernel, dim3(M), dim3(kThreads), 0, st, x, xh, xl, rsc, K);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  switch (p.cfg) {
+    case 0: e = launch_gemm<1, 4, 1, 2>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st); break;
+    case 1: e = launch_gemm<2, 2, 1, 2>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st); break;
+    default: e = launch_gemm<2, 2, 2, 2>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st); break;
+  }
+  if (e != hipSuccess || p.splits == 1) return e;
+  const size_t count = static_cast<size_t>(M) * N;
+  const int grid = static_cast<int>(std::min<size_t>((count + kThreads - 1) / kThreads, 4096));
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid), dim3(kThreads), 0, st, part, y, count,
+                     p.splits);
+  return hipGetLastError();
+}
+
+}  // namespace sq8

@@ -61,6 +61,18 @@ def test_workspace_too_small_is_rejected(sq8):
 
 def test_path_selection(sq8):
     assert sq8.path_name(1, 4096, 4096, 64) == "gemv"
+    assert sq8.path_name(2, 4096, 4096, 64) == "gemv"
+    assert sq8.path_name(3, 4096, 4096, 64) == "mfma"
+    assert sq8.path_name(2048, 4096, 4096, 64) == "mfma"
+    assert sq8.path_name(8, 4096, 4096, 32) == "gemv"      # MFMA steps are whole 64-wide groups
     assert sq8.path_name(1, 4096, 100, 4) == "generic"   # gs not a multiple of 16
     assert sq8.path_name(1, 16, 100, 64) == "generic"    # K not a multiple of gs
     assert sq8.path_name(0, 16, 64, 64) == "invalid"
+
+
+def test_workspace_sizes(sq8):
+    assert sq8.workspace_bytes(1, 4096, 4096, 64) == 0
+    # MFMA path: f16 hi/lo copies of x (4*M*K bytes) plus row scales, plus split-K partials
+    for M in (8, 64, 2048):
+        assert sq8.workspace_bytes(M, 4096, 4096, 64) >= 4 * M * 4096
+    assert sq8.workspace_bytes(0, 4096, 4096, 64) == 0
