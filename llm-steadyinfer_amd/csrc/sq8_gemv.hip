@@ -148,7 +148,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const float* __restric
 
   i32x4 qa[U][R], qb[U][R];
   float sa[U][R], sb[U][R];
-  auto load = [&](int b, int st, i32x4 (&q)[U][R], float (&sc)[U][R]) {
+  auto load = [&](int b, int st, i32x4 (&q)[U][R], float (&sc)[U][R]) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = (st * U + u) * 1024 + lane * 16;
@@ -167,7 +167,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const float* __restric
   float acc[R * MT];
 #pragma unroll
   for (int i = 0; i < R * MT; ++i) acc[i] = 0.f;
-  auto consume = [&](int b, int st, const i32x4 (&q)[U][R], const float (&sc)[U][R]) {
+  auto consume = [&](int b, int st, const i32x4 (&q)[U][R], const float (&sc)[U][R]) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = (st * U + u) * 1024 + lane * 16;

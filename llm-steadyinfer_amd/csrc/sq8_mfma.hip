@@ -20,6 +20,7 @@
 //  * Skinny shapes (few tokens, few output tiles) split K over gridDim.z; partial tiles go to the
 //    workspace and a second kernel sums them in split order (deterministic).
 #include <algorithm>
+#include <type_traits>
 
 #include "sq8_common.h"
 
@@ -150,7 +151,7 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
 
   u32x4 rxh[T::XCH], rxl[T::XCH], rw[T::WCH];
   float rs[TN];
-  auto gload = [&](int st) {
+  auto gload = [&](int st) __attribute__((always_inline)) {
     const int k0 = st * BK;
 #pragma unroll
     for (int i = 0; i < T::XCH; ++i) {
@@ -163,7 +164,7 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
 #pragma unroll
     for (int j = 0; j < TN; ++j) rs[j] = s_src[j][k0 / gs];
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf) __attribute__((always_inline)) {
     _Float16* sxh = lds + buf * T::STAGE_HALVES;
     _Float16* sxl = sxh + T::BM * LDS_STRIDE;
     _Float16* sw = sxl + T::BM * LDS_STRIDE;
@@ -272,6 +273,248 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
   }
 }
 
+// Split-K tickets live at the start of the workspace; each call leaves them zero.
+constexpr int kTicketBytes = 64 * 1024;  // ticket array at the start of the workspace
+
+// ---------------------------------------------------------------- skinny decode kernel
+// For 3 <= M <= 64 token rows: one launch, no activation prologue, v_mfma_f32_16x16x32_f16 on
+// MT16 stacked 16-row tiles. A workgroup (4 waves) owns BN = 64*TN output columns, all M rows and
+// a range of K groups (its split), walked in chunks of KW groups. A wave owns only 16*TN columns,
+// so many waves are in flight per CU, which is what hides HBM latency at these sizes:
+//  * the wave's weights go from HBM straight into MFMA B registers, double-buffered across
+//    chunks; scales ride with them;
+//  * the M x (64*KW) activation chunk is split to f16 hi/lo in LDS once per chunk with one power
+//    of two per (row, group) from that row's group absmax, so any activation range is safe;
+//  * per group, acc += (scale[n, g] * 2^-e[m, g]) * P for the group product P;
+//  * lane l: weight row n0 + l%16, the 16 contiguous bytes (l/16)*16.. of each 64-wide group (one
+//    dwordx4 per lane per group; a wave instruction covers 16 rows x 64 B);
+//  * A operand for step t in {0,1}: x[m = l%16][(l/16)*16 + 8t .. +8] from LDS (hi, lo);
+//  * result lane l: column l%16, rows 4*(l/16) .. +3.
+// Split-K partials are exchanged with agent-scope relaxed atomic stores and loads (coherent across
+// the XCDs' L2s without a cache writeback); each thread waits for its stores to be acknowledged
+// before the workgroup takes its ticket.
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+template <int MR, int KW, int TN, int MT16>
+__global__ __launch_bounds__(kThreads) void skinny16_kernel(
+    const float* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ s,
+    float* __restrict__ y, float* __restrict__ part, unsigned* __restrict__ tickets, int M, int N,
+    int K, int gs, int gps, int splits) {
+  constexpr int BMP = 16 * MT16;                   // MFMA rows: MT16 stacked 16-row tiles
+  static_assert(MR <= BMP && (MR == 8 || MR % 16 == 0), "rows loaded per chunk");
+  constexpr int BN = 4 * TN * 16;                  // 4 waves x TN tiles of 16 columns
+  constexpr int XF4 = MR * KW * 16 / kThreads;     // float4 of an activation chunk per thread
+  static_assert(XF4 >= 1, "chunk too small for the staging pattern");
+  constexpr int GROUP_HALVES = BMP * LDS_STRIDE;
+  __shared__ __attribute__((aligned(16))) _Float16 sxh[2][KW * GROUP_HALVES];
+  __shared__ __attribute__((aligned(16))) _Float16 sxl[2][KW * GROUP_HALVES];
+  __shared__ __attribute__((aligned(16))) float sxs[2][KW * BMP];
+  __shared__ int is_last;
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int lcol = lane & 15, kq = (lane >> 4) * 16;
+  const int n0 = blockIdx.x * BN;
+  const int gbeg = blockIdx.y * gps;
+  const int nch = (min(K / BK, gbeg + gps) - gbeg) / KW;
+  const int gpr = K / gs;
+
+  if (MR < BMP) {  // rows MR..15 of both buffers are never loaded: zero them once
+    for (int i = tid; i < 2 * KW * (BMP - MR) * LDS_STRIDE; i += kThreads) {
+      const int b = i / (KW * (BMP - MR) * LDS_STRIDE), r = i % (KW * (BMP - MR) * LDS_STRIDE);
+      const int q = r / ((BMP - MR) * LDS_STRIDE), o = r % ((BMP - MR) * LDS_STRIDE);
+      sxh[b][q * GROUP_HALVES + MR * LDS_STRIDE + o] = static_cast<_Float16>(0.f);
+      sxl[b][q * GROUP_HALVES + MR * LDS_STRIDE + o] = static_cast<_Float16>(0.f);
+    }
+    for (int i = tid; i < 2 * KW * (BMP - MR); i += kThreads) {
+      const int b = i / (KW * (BMP - MR)), r = i % (KW * (BMP - MR));
+      sxs[b][(r / (BMP - MR)) * BMP + MR + r % (BMP - MR)] = 0.f;
+    }
+  }
+
+  const int8_t* wsrc[TN];
+  const float* ssrc[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int ncol = min(n0 + (wave * TN + j) * 16 + lcol, N - 1);
+    wsrc[j] = w + static_cast<size_t>(ncol) * K + static_cast<size_t>(gbeg) * BK + kq;
+    ssrc[j] = s + static_cast<size_t>(ncol) * gpr;
+  }
+
+  u32x4 wr[2][KW][TN];
+  float wsc[2][KW][TN];
+  auto wload = [&](int b, int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < KW; ++q)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        wr[b][q][j] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(wsrc[j] + (c * KW + q) * BK));
+        wsc[b][q][j] = ssrc[j][((gbeg + c * KW + q) * BK) / gs];
+      }
+  };
+  float4 xr[XF4];
+  auto xload = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < XF4; ++i) {
+      const int f = tid + kThreads * i;
+      const int row = f / (KW * 16), rem = f % (KW * 16);
+      xr[i] = *reinterpret_cast<const float4*>(x + static_cast<size_t>(min(row, M - 1)) * K +
+                                               (gbeg + c * KW) * BK + rem * 4);
+    }
+  };
+  auto xstore = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < XF4; ++i) {
+      const int f = tid + kThreads * i;
+      const int row = f / (KW * 16), rem = f % (KW * 16), q = rem >> 4, part4 = rem & 15;
+      const float4 v = row < M ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+      for (int off = 8; off >= 1; off /= 2) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+      int e = 0;
+      if (amax > 0.f && amax <= 3.402823466e38f) {
+        int ex;
+        frexpf(amax, &ex);
+        e = min(max(14 - ex, -126), 126);
+      }
+      const float a[4] = {ldexpf(v.x, e), ldexpf(v.y, e), ldexpf(v.z, e), ldexpf(v.w, e)};
+      _Float16 h[4], l[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        h[c] = static_cast<_Float16>(a[c]);
+        l[c] = static_cast<_Float16>(a[c] - static_cast<float>(h[c]));
+      }
+      const int o = q * GROUP_HALVES + row * LDS_STRIDE + part4 * 4;
+      *reinterpret_cast<uint2*>(&sxh[b][o]) = *reinterpret_cast<const uint2*>(h);
+      *reinterpret_cast<uint2*>(&sxl[b][o]) = *reinterpret_cast<const uint2*>(l);
+      if (part4 == 0) sxs[b][q * BMP + row] = ldexpf(1.f, -e);
+    }
+  };
+
+  f4v acc[MT16][TN];
+#pragma unroll
+  for (int i = 0; i < MT16; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f4v{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < KW; ++q) {
+      h8 bw[TN][2];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        uint32_t hq[8];
+        i8x4_to_h4(wr[b][q][j].x, hq[0], hq[1]);
+        i8x4_to_h4(wr[b][q][j].y, hq[2], hq[3]);
+        i8x4_to_h4(wr[b][q][j].z, hq[4], hq[5]);
+        i8x4_to_h4(wr[b][q][j].w, hq[6], hq[7]);
+        const u32x4 b0 = {hq[0], hq[1], hq[2], hq[3]};
+        const u32x4 b1 = {hq[4], hq[5], hq[6], hq[7]};
+        bw[j][0] = __builtin_bit_cast(h8, b0);
+        bw[j][1] = __builtin_bit_cast(h8, b1);
+      }
+#pragma unroll
+      for (int i = 0; i < MT16; ++i) {
+        const int o = q * GROUP_HALVES + (i * 16 + lcol) * LDS_STRIDE + kq;
+        const h8 ah0 = *reinterpret_cast<const h8*>(&sxh[b][o]);
+        const h8 al0 = *reinterpret_cast<const h8*>(&sxl[b][o]);
+        const h8 ah1 = *reinterpret_cast<const h8*>(&sxh[b][o + 8]);
+        const h8 al1 = *reinterpret_cast<const h8*>(&sxl[b][o + 8]);
+        const float4 rs =
+            *reinterpret_cast<const float4*>(&sxs[b][q * BMP + i * 16 + (lane >> 4) * 4]);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const f4v zero = {0.f, 0.f, 0.f, 0.f};
+          f4v p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah0, bw[j][0], zero, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(al0, bw[j][0], p, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah1, bw[j][1], p, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(al1, bw[j][1], p, 0, 0, 0);
+          const float sc = wsc[b][q][j];
+          acc[i][j][0] = fmaf(sc * rs.x, p[0], acc[i][j][0]);
+          acc[i][j][1] = fmaf(sc * rs.y, p[1], acc[i][j][1]);
+          acc[i][j][2] = fmaf(sc * rs.z, p[2], acc[i][j][2]);
+          acc[i][j][3] = fmaf(sc * rs.w, p[3], acc[i][j][3]);
+        }
+      }
+    }
+  };
+
+  // Chunk c: weights in wr[c & 1], activations in LDS buffer c & 1. The next chunk's activation
+  // loads are issued before its weight loads (a scheduling barrier keeps that order): vmcnt
+  // retires in issue order, so waiting for the activations leaves the weight prefetch in flight.
+  if (nch > 0) {
+    xload(0);
+    wload(0, 0);
+    xstore(0);
+  }
+  __syncthreads();
+  auto step = [&](auto buf, int c) __attribute__((always_inline)) {
+    constexpr int B = decltype(buf)::value;
+    const bool more = c + 1 < nch;
+    if (more) xload(c + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (more) wload(B ^ 1, c + 1);
+    compute(B);
+    if (more) xstore(B ^ 1);
+    __syncthreads();
+  };
+  for (int c = 0; c < nch;) {
+    step(std::integral_constant<int, 0>{}, c);
+    if (++c >= nch) break;
+    step(std::integral_constant<int, 1>{}, c);
+    ++c;
+  }
+
+  if (splits == 1) {
+#pragma unroll
+    for (int t = 0; t < MT16; ++t)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int n = n0 + (wave * TN + j) * 16 + lcol;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = t * 16 + (lane >> 4) * 4 + i;
+          if (m < M && n < N) y[static_cast<size_t>(m) * N + n] = acc[t][j][i];
+        }
+      }
+    return;
+  }
+  float* dst = part + static_cast<size_t>(blockIdx.y) * M * N;
+#pragma unroll
+  for (int t = 0; t < MT16; ++t)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + (wave * TN + j) * 16 + lcol;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = t * 16 + (lane >> 4) * 4 + i;
+        if (m < M && n < N)
+          __hip_atomic_store(dst + static_cast<size_t>(m) * N + n, acc[t][j][i],
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  // Wait until this thread's partial stores are acknowledged (s_waitcnt with every counter at
+  // zero) before the workgroup takes its ticket.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0)
+    is_last = __hip_atomic_fetch_add(&tickets[blockIdx.x], 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) == static_cast<unsigned>(splits - 1);
+  __syncthreads();
+  if (!is_last) return;
+  const int ncols = min(BN, N - n0);
+  for (int idx = tid; idx < M * ncols; idx += kThreads) {
+    const int m = idx / ncols, nn = n0 + idx % ncols;
+    const size_t o = static_cast<size_t>(m) * N + nn;
+    float v = __hip_atomic_load(part + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int z = 1; z < splits; ++z)
+      v += __hip_atomic_load(part + static_cast<size_t>(z) * M * N + o, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    y[o] = v;
+  }
+  if (tid == 0)
+    __hip_atomic_store(&tickets[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Sum split-K partials in split order: y[i] = sum_z part[z][i].
 __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(const float* __restrict__ part,
                                                                 float* __restrict__ y,
@@ -286,8 +529,13 @@ __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(const float* __
 
 size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 
+// Largest M served by the single-launch skinny kernel.
+constexpr int kSkinnyMaxM = 32;
+
 struct Plan {
-  int cfg;        // 0: 32x256 tile, 1: 64x128, 2: 128x128
+  bool skinny;
+  int kw;         // skinny: K groups per chunk (divides groups_per_split)
+  int cfg;        // GEMM: 0: 32x256 tile, 1: 64x128, 2: 128x128.  Skinny: 0: MT=1, 1: MT=2
   int bm, bn;
   int splits;
   int groups_per_split;
@@ -295,12 +543,31 @@ struct Plan {
 
 Plan make_plan(int M, int N, int K) {
   Plan p{};
+  const int nsteps = K / BK;
+  const int target = 2 * cu_count();
+  if (M <= kSkinnyMaxM) {
+    p.skinny = true;
+    p.cfg = 0;
+    p.bm = M <= 8 ? 8 : ((M + 15) / 16) * 16;
+    p.bn = 64;
+    const int blocks = (N + p.bn - 1) / p.bn;
+    const int kw_max = M <= 32 ? 4 : 2;
+    const int target_wg = target;
+    p.kw = 1;
+    while (p.kw < kw_max && nsteps % (2 * p.kw) == 0) p.kw *= 2;
+    const int chunks = nsteps / p.kw;
+    int splits = 1;
+    if (blocks < target_wg && blocks <= kTicketBytes / 4)
+      splits = min(chunks, (target_wg + blocks - 1) / blocks);
+    const int cps = (chunks + splits - 1) / splits;  // chunks per split
+    p.groups_per_split = cps * p.kw;
+    p.splits = (chunks + cps - 1) / cps;
+    return p;
+  }
   if (M <= 32) { p.cfg = 0; p.bm = 32; p.bn = 256; }
   else if (M <= 64) { p.cfg = 1; p.bm = 64; p.bn = 128; }
   else { p.cfg = 2; p.bm = 128; p.bn = 128; }
   const int tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
-  const int nsteps = K / BK;
-  const int target = 2 * cu_count();
   int splits = 1;
   if (tiles < target) splits = min(min(16, nsteps), (target + tiles - 1) / tiles);
   p.groups_per_split = (nsteps + splits - 1) / splits;
@@ -328,12 +595,27 @@ hipError_t launch_gemm(const _Float16* xh, const _Float16* xl, const float* rsc,
   return hipGetLastError();
 }
 
+template <int MR, int KW, int TN = 1, int MT16 = 1>
+hipError_t launch_skinny16(const float* x, const int8_t* w, const float* s, float* y, float* part,
+                           unsigned* tickets, int M, int N, int K, int gs, const Plan& p,
+                           hipStream_t st) {
+  const dim3 grid((N + 64 * TN - 1) / (64 * TN), p.splits);
+  hipLaunchKernelGGL((skinny16_kernel<MR, KW, TN, MT16>), grid, dim3(kThreads), 0, st, x, w, s, y, part,
+                     tickets, M, N, K, gs, p.groups_per_split, p.splits);
+  return hipGetLastError();
+}
+
 }  // namespace
 
+// Workspace layout: [ticket array, kTicketBytes][path buffers]. The ticket array must be zero
+// before the first call; every call leaves it zero.
 size_t mfma_workspace_bytes(int M, int N, int K) {
   const Plan p = make_plan(M, N, K);
-  size_t b = 2 * align256(static_cast<size_t>(M) * K * sizeof(_Float16));
-  b += align256(static_cast<size_t>(M) * sizeof(float));
+  size_t b = kTicketBytes;
+  if (!p.skinny) {
+    b += 2 * align256(static_cast<size_t>(M) * K * sizeof(_Float16));
+    b += align256(static_cast<size_t>(M) * sizeof(float));
+  }
   if (p.splits > 1) b += align256(static_cast<size_t>(p.splits) * M * N * sizeof(float));
   return b;
 }
@@ -343,7 +625,26 @@ size_t mfma_workspace_bytes(int M, int N, int K) {
 hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
                        int K, int gs, void* ws, hipStream_t st) {
   const Plan p = make_plan(M, N, K);
-  char* base = static_cast<char*>(ws);
+  unsigned* tickets = static_cast<unsigned*>(ws);
+  char* base = static_cast<char*>(ws) + kTicketBytes;
+  if (p.skinny) {
+    float* part = reinterpret_cast<float*>(base);
+#define SQ8_SKINNY(MR, MT16)                                                               \
+  switch (p.kw) {                                                                          \
+    case 4: return launch_skinny16<MR, 4, 1, MT16>(x, w, s, y, part, tickets, M, N, K, gs, p, st); \
+    case 2: return launch_skinny16<MR, 2, 1, MT16>(x, w, s, y, part, tickets, M, N, K, gs, p, st); \
+    default: return launch_skinny16<MR, 1, 1, MT16>(x, w, s, y, part, tickets, M, N, K, gs, p, st); \
+  }
+    if (M <= 8 && p.kw == 4)
+      return launch_skinny16<8, 4, 1, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st);
+    if (M <= 8 && p.kw == 2)
+      return launch_skinny16<8, 2, 1, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st);
+    if (M <= 16) SQ8_SKINNY(16, 1);
+    if (M <= 32) SQ8_SKINNY(32, 2);
+    if (M <= 48) SQ8_SKINNY(48, 3);
+    SQ8_SKINNY(64, 4);
+#undef SQ8_SKINNY
+  }
   _Float16* xh = reinterpret_cast<_Float16*>(base);
   base += align256(static_cast<size_t>(M) * K * sizeof(_Float16));
   _Float16* xl = reinterpret_cast<_Float16*>(base);

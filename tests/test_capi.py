@@ -72,7 +72,8 @@ def test_path_selection(sq8):
 
 def test_workspace_sizes(sq8):
     assert sq8.workspace_bytes(1, 4096, 4096, 64) == 0
-    # MFMA path: f16 hi/lo copies of x (4*M*K bytes) plus row scales, plus split-K partials
+    # MFMA paths: split-K tickets and partials; the GEMM path adds f16 hi/lo copies of x (4*M*K B)
     for M in (8, 64, 2048):
-        assert sq8.workspace_bytes(M, 4096, 4096, 64) >= 4 * M * 4096
+        assert sq8.workspace_bytes(M, 4096, 4096, 64) > 0
+    assert sq8.workspace_bytes(2048, 4096, 4096, 64) >= 4 * 2048 * 4096
     assert sq8.workspace_bytes(0, 4096, 4096, 64) == 0

@@ -150,3 +150,37 @@ def test_special_values(sq8, dev):
     y = run(sq8, dev, x, q, s, 64)
     exp = (s.reshape(N, -1)[:, 130 // 64] * q[:, 130].astype(np.float32)).astype(np.float32)
     np.testing.assert_array_equal(y[1], exp)
+
+
+@pytest.mark.parametrize("M", [1, 3, 8, 40, 64, 100, 256])
+def test_activation_dynamic_range(sq8, dev, M):
+    """Token rows whose magnitudes span 1e-30 .. 1e30 each stay within tolerance of their own row
+    (the f16 hi/lo split scales every row/group by its own power of two)."""
+    N, K = 96, 1024
+    x, q, s = o.make_case(M, N, K, 64, seed=100 + M)
+    mags = np.array([1e-30, 1e-5, 1.0, 3e4, 1e30, 7e-3, 2.0, 1e10], np.float32)
+    x = (x * mags[np.arange(M) % len(mags)][:, None]).astype(np.float32)
+    y = run(sq8, dev, x, q, s, 64)
+    ref = o.matmul_f64(x, q, s, 64)
+    for m in range(M):
+        check(y[m:m + 1], ref[m:m + 1], f"row {m} scale {mags[m % len(mags)]:.0e}")
+
+
+def test_split_k_tickets_return_to_zero(sq8, dev):
+    """Skinny split-K calls leave the workspace ticket array zero and are bitwise repeatable."""
+    import torch
+    M, N, K = 16, 4096, 4096
+    x, q, s = o.make_case(M, N, K, 64, seed=3)
+    ws = sq8.Workspace(dev)
+    xt, qt, st = (torch.from_numpy(a).to(dev) for a in (x, q, s))
+    ys = []
+    for _ in range(3):
+        ys.append(sq8.matmul(xt, qt, st, group_size=64, workspace=ws).cpu().numpy())
+    torch.cuda.synchronize()
+    assert int(ws.buf[:65536].count_nonzero()) == 0
+    np.testing.assert_array_equal(ys[0], ys[1])
+    np.testing.assert_array_equal(ys[0], ys[2])
+    rows = _row_subset(N, 100, seed=4)
+    ref = o.matmul_f64(x, np.ascontiguousarray(q[rows]),
+                       np.ascontiguousarray(s.reshape(N, -1)[rows].reshape(-1)), 64)
+    check(ys[0][:, rows], ref, "split-k M=16")
