@@ -10,7 +10,12 @@ weight in the 256 MB Infinity Cache. `value` is algorithmic bytes per step / ste
 Also reported: the per-launch GB/s and TFLOP/s of every (projection, M) pair of configs 2 and 3,
 the roofline of the dominant kernel, and the CPU oracle's throughput on a bounded sample.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
+The step's 129 launches are issued eagerly on one stream; `--graph` replays them as one HIP graph
+instead (the reference captures its decode step in a CUDA graph, src/source/model/model.cpp:
+189-238). On MI355X the eager launches measured faster, so eager is the default.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu] [--graph]
+       python bench.py --profile   # short run for rocprofv3 counter passes (see profiles/)
 """
 from __future__ import annotations
 
@@ -28,7 +33,10 @@ HIDDEN, FFN, VOCAB, LAYERS = 4096, 14336, 128256, 32
 PROJ = {"qkv": (6144, HIDDEN), "o": (HIDDEN, HIDDEN), "gate_up": (2 * FFN, HIDDEN),
         "down": (HIDDEN, FFN)}
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
-MFMA_FP32_PEAK_TFLOPS = 157.3  # dense fp32 matrix peak
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16 matrix peak (the prefill GEMM issues f16 MFMA)
+# HBM bytes per M=1 GEMV launch over algorithmic bytes, from rocprofv3 FETCH_SIZE/WRITE_SIZE passes
+# over `python bench.py --profile`, scaled by a 256 MiB copy of known size (profiles/).
+GEMV_TRAFFIC_RATIO = 1.005
 METRIC = "INT8 GEMV HBM GB/s (% of peak) + decode tokens/s, Llama-3-8B shapes, 1 GPU"
 
 
@@ -118,6 +126,9 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--graph", action="store_true", help="replay the step as one HIP graph")
+    ap.add_argument("--profile", action="store_true",
+                    help="short run for counter collection: a 256 MiB copy, then 5 decode steps")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -129,7 +140,8 @@ def main():
     sq8.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    stream = torch.cuda.current_stream(dev)
+    stream = torch.cuda.Stream(dev)  # default priority
+    torch.cuda.set_stream(stream)
     ws = sq8.Workspace(dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(5678)
@@ -162,35 +174,60 @@ def main():
         for c in calls:
             c()
 
+    if args.profile:
+        # Calibration copy of known size for FETCH_SIZE / WRITE_SIZE, then a few decode steps.
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            step()
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_run": True, "launches_per_step": len(calls),
+                          "step_algo_bytes": step_bytes}))
+        return
+
+    def timed(fn, steps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / args.steps
+    dt_eager = timed(step, args.steps)
+    dt_graph = None
+    if args.graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            step()
+        for _ in range(args.warmup):
+            graph.replay()
+        dt_graph = timed(graph.replay, args.steps)
+    dt = dt_graph if args.graph else dt_eager
     value = step_bytes / dt / 1e9
 
-    # Per-launch kernel time of the dominant kernel (the M=1 GEMV) with HIP events on the stream
-    # the kernels run on, over further steps.
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in calls]
-    kern_ms, kern_bytes, nlaunch = 0.0, 0, 0
-    for _ in range(3):
-        for c, (a, b) in zip(calls, ev):
-            a.record(stream)
-            c()
-            b.record(stream)
-        torch.cuda.synchronize()
-        kern_ms += sum(a.elapsed_time(b) for a, b in ev)
-        kern_bytes += step_bytes
-        nlaunch += len(calls)
-    achieved = kern_bytes / (kern_ms / 1e3) / 1e9
+    # Average launch duration of the dominant kernel (the M=1 decode GEMV: every launch of the
+    # step) from HIP events on the stream the kernels run on, around further eager steps.
+    reps = max(3, args.steps // 2)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    launch_us = e0.elapsed_time(e1) * 1e3 / (reps * len(calls))
+    bytes_per_launch = step_bytes / len(calls)
+    achieved = bytes_per_launch / launch_us / 1e3
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "sq8 gemv_rows_kernel<8,1,64> (M=1)",
-                "avg_launch_us": round(kern_ms * 1e3 / nlaunch, 2),
-                "algo_bytes_per_launch": round(kern_bytes / nlaunch)}
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": round(bytes_per_launch * GEMV_TRAFFIC_RATIO),
+                "kernel": "sq8 stream_kernel, M=1 decode GEMV (<2,4,1,64> for K=4096, "
+                          "<2,2,1,64> for K=14336)",
+                "avg_launch_us": round(launch_us, 3),
+                "algo_bytes_per_launch": round(bytes_per_launch)}
 
     # ---------------------------------------------------------------- configs 2 and 3 sweep
     sweep = []
@@ -208,9 +245,14 @@ def main():
                 b.record(stream)
                 torch.cuda.synchronize()
                 us = a.elapsed_time(b) * 1e3 / reps
-                sweep.append({"proj": p, "M": M, "N": N, "K": K, "path": sq8.path_name(M, N, K, GS),
-                              "us": round(us, 2), "GB/s": round(cs[0].bytes / us / 1e3, 1),
-                              "TFLOP/s": round(cs[0].flops / us / 1e6, 2)})
+                tflops = cs[0].flops / us / 1e6
+                rec = {"proj": p, "M": M, "N": N, "K": K, "path": sq8.path_name(M, N, K, GS),
+                       "us": round(us, 2), "GB/s": round(cs[0].bytes / us / 1e3, 1),
+                       "TFLOP/s": round(tflops, 2)}
+                if sq8.path_name(M, N, K, GS) == "mfma":
+                    # the f16 MFMA path issues two products (hi and lo) per useful multiply-add
+                    rec["mfma_frac"] = round(2 * tflops / MFMA_F16_PEAK_TFLOPS, 4)
+                sweep.append(rec)
                 del x, y, cs
             print(f"# sweep M={M} done", file=sys.stderr, flush=True)
 
@@ -227,6 +269,8 @@ def main():
                                "o 4096x4096, gate_up 28672x4096, down 4096x14336) + lm_head "
                                "128256x4096, group 64", "global_batch": 1, "parallelism": "none"},
         "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        "launch": "hip_graph" if args.graph else "eager",
+        "graph_GBps": round(step_bytes / dt_graph / 1e9, 1) if dt_graph else None,
         "decode_matmul_tokens_per_s": round(1.0 / dt, 1),
         "step_algo_bytes": step_bytes,
         "roofline": roofline,
