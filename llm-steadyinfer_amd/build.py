@@ -16,6 +16,11 @@ REPO_DIR = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 OBJ_DIR = PKG_DIR / "_build"
 LIB_PATH = PKG_DIR / "libsq8.so"
+CPP_DIR = PKG_DIR / "cpp"
+OP_LIB_PATH = PKG_DIR / "libsq8_op.so"
+CPP_TEST_SRC = REPO_DIR / "tests" / "cpp" / "test_matmul_layer.cpp"
+CPP_TEST_BIN = OBJ_DIR / "test_matmul_layer"
+ORACLE_LIB = REPO_DIR / "oracle" / "_ref" / "libsq8_oracle.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -25,9 +30,9 @@ COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall",
                 "-Wno-unused-result", "-I", str(REPO_DIR / "include"), "-I", str(CSRC)]
 
 
-def _compile(src: Path) -> Path:
-    obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, extra=()) -> Path:
+    obj = OBJ_DIR / (src.parent.name + "_" + src.stem + ".o")
+    cmd = [HIPCC, *COMMON_FLAGS, *extra, *DEVICE_FLAGS, "-x", "hip", "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
@@ -39,6 +44,43 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+def _link(objs, out: Path, extra=()):
+    tmp = out.with_suffix(out.suffix + ".tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", *map(str, objs), *extra, "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link of {out.name} failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
+
+
+def build_op_layer(verbose: bool = False) -> Path:
+    """Compile the C++ op API (Tensor, MatmulLayer, get_matmul_kernel_quant8) into libsq8_op.so,
+    linked against libsq8.so."""
+    srcs = sorted((CPP_DIR / "src").glob("*.cpp")) + sorted((CPP_DIR / "src").glob("*.hip"))
+    inc = ["-I", str(CPP_DIR / "include")]
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = list(ex.map(lambda p: _compile(p, inc), srcs))
+    _link(objs, OP_LIB_PATH, ["-shared", "-fPIC", "-L", str(PKG_DIR), "-lsq8",
+                              "-Wl,-rpath,$ORIGIN"])
+    if verbose:
+        print(f"built {OP_LIB_PATH}")
+    return OP_LIB_PATH
+
+
+def build_cpp_tests(verbose: bool = False) -> Path:
+    """Compile the C++ op-layer test program (links libsq8_op.so, libsq8.so and the oracle)."""
+    if not ORACLE_LIB.exists():
+        raise RuntimeError(f"oracle library missing: {ORACLE_LIB}")
+    inc = ["-I", str(CPP_DIR / "include")]
+    obj = _compile(CPP_TEST_SRC, inc)
+    _link([obj], CPP_TEST_BIN, ["-L", str(PKG_DIR), "-lsq8_op", "-lsq8", "-L",
+                                 str(ORACLE_LIB.parent), "-lsq8_oracle",
+                                 "-Wl,-rpath,$ORIGIN/..", "-Wl,-rpath,$ORIGIN/../../oracle/_ref"])
+    if verbose:
+        print(f"built {CPP_TEST_BIN}")
+    return CPP_TEST_BIN
+
+
 def build(verbose: bool = False) -> Path:
     """Compile all HIP sources and link ``libsq8.so``; returns the library path."""
     OBJ_DIR.mkdir(exist_ok=True)
@@ -47,14 +89,10 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
+    _link(objs, LIB_PATH, ["-shared", "-fPIC"])
     if verbose:
         print(f"built {LIB_PATH}")
+    build_op_layer(verbose)
     return LIB_PATH
 
 
