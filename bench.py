@@ -1,14 +1,16 @@
 #!/usr/bin/env python3
 """Benchmark of the gfx950 INT8 group-quant matmul path on one MI355X.
 
-A "step" is the INT8 matmul work of one Llama-3-8B decode token at batch 1 (BASELINE config 2 at
-M=1): for each of the 32 layers the fused QKV (6144x4096), O (4096x4096), fused gate/up
+A "step" is the INT8 matmul work of one Llama-3-8B decode token at batch 1 (the batched-decode
+configuration at M=1): for each of the 32 layers the fused QKV (6144x4096), O (4096x4096), fused gate/up
 (28672x4096) and down (4096x14336) projections, then the LM head (128256x4096). All 129 weights
 are distinct random-init INT8 tensors resident in HBM (7.97 GB with scales), so no launch finds its
 weight in the 256 MB Infinity Cache. `value` is algorithmic bytes per step / step time (GB/s).
 
-Also reported: the per-launch GB/s and TFLOP/s of every (projection, M) pair of configs 2 and 3,
+Also reported: the per-launch GB/s and TFLOP/s of every (projection, M) pair of the batched-decode
+(M in 1, 8, 32, 64) and prefill (M = 2048) configurations,
 the roofline of the dominant kernel, and the CPU oracle's throughput on a bounded sample.
+Counter runs: `python bench.py --profile` (see profiles/ for the rocprofv3 commands).
 
 The step's 129 launches are issued eagerly on one stream; `--graph` replays them as one HIP graph
 instead (the reference captures its decode step in a CUDA graph, src/source/model/model.cpp:
@@ -131,8 +133,9 @@ def main():
                     help="short run for counter collection: a 256 MiB copy, then 5 decode steps")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the matmul would shard by output rows / K groups, see DESIGN.md).", file=sys.stderr)
+        print("bench.py measures one GPU only: this build has no multi-GPU path. The matmul "
+              "would shard column-parallel by output rows (qkv, gate/up, lm_head) and "
+              "row-parallel by 64-aligned K groups (o, down) with one all-reduce.", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -24,7 +24,7 @@ ORACLE_LIB = REPO_DIR / "oracle" / "_ref" / "libsq8_oracle.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
-# Packed fp32 VALU instructions are disabled for every device compile (traps).
+# Packed fp32 VALU instructions (v_pk_*_f32) are disabled for every device compile.
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall",
                 "-Wno-unused-result", "-I", str(REPO_DIR / "include"), "-I", str(CSRC)]
