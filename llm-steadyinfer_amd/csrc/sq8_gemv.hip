@@ -148,7 +148,11 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const float* __restric
 
   i32x4 qa[U][R], qb[U][R];
   float sa[U][R], sb[U][R];
+  // Loads are issued unconditionally (a step past the last block reads the first bytes of x, which
+  // are cached, and is never consumed): with no branch around them the compiler's wait counts stay
+  // exact, so waiting for one step never drains the prefetch of the next.
   auto load = [&](int b, int st, i32x4 (&q)[U][R], float (&sc)[U][R]) __attribute__((always_inline)) {
+    const bool live = b < nblk;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int k = (st * U + u) * 1024 + lane * 16;
@@ -157,10 +161,12 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const float* __restric
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int n = min(b * R + r, N - 1);
-        const i32x4 v =
-            __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(w + static_cast<size_t>(n) * K + kc));
+        const i32x4* wp = live ? reinterpret_cast<const i32x4*>(w + static_cast<size_t>(n) * K + kc)
+                               : reinterpret_cast<const i32x4*>(x);
+        const float* sp = live ? s + static_cast<size_t>(n) * gpr + kc / gs : x;
+        const i32x4 v = __builtin_nontemporal_load(wp);
         q[u][r] = ok ? v : i32x4{0, 0, 0, 0};
-        sc[u][r] = s[static_cast<size_t>(n) * gpr + kc / gs];
+        sc[u][r] = *sp;
       }
     }
   };
@@ -174,8 +180,10 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const float* __restric
       const int kc = k < K ? k : 0;
 #pragma unroll
       for (int t = 0; t < MT; ++t) {
-        const float4* xp = reinterpret_cast<const float4*>(xs + t * K + kc);
-        const float4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+        const int i0 = (t * K + kc) / 4;  // float4 number of the chunk's first 4 elements
+        const float4* xp = reinterpret_cast<const float4*>(xs) + i0;
+        const int sw = (i0 >> 4) & 3;      // the staging swizzle of float4 numbers i0 .. i0+3
+        const float4 x0 = xp[0 ^ sw], x1 = xp[1 ^ sw], x2 = xp[2 ^ sw], x3 = xp[3 ^ sw];
 #pragma unroll
         for (int r = 0; r < R; ++r)
           acc[r * MT + t] = fmaf(sc[u][r], dot16(q[u][r], x0, x1, x2, x3), acc[r * MT + t]);
@@ -195,15 +203,17 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const float* __restric
   };
 
   int b = gw, st = 0;
-  if (b < nblk) load(b, st, qa, sa);
-  // Stage x after the first weight loads are in flight.
-  for (int i = tid * 4; i < MT * K; i += kThreads * 4)
-    *reinterpret_cast<float4*>(xs + i) = *reinterpret_cast<const float4*>(x + i);
+  load(b, st, qa, sa);
+  // Stage x after the first weight loads are in flight. float4 number i is stored at
+  // i ^ ((i >> 4) & 3): a lane reads the 4 float4 of its 16-element chunk, and without the swizzle
+  // lanes l and l+4 would hit the same LDS banks in every ds_read_b128 (4-way conflicts).
+  for (int i = tid; i < MT * K / 4; i += kThreads)
+    reinterpret_cast<float4*>(xs)[i ^ ((i >> 4) & 3)] = reinterpret_cast<const float4*>(x)[i];
   __syncthreads();
   while (b < nblk) {
     int b1 = b, st1 = st + 1;
     if (st1 == nsteps) { st1 = 0; b1 += GW; }
-    if (b1 < nblk) load(b1, st1, qb, sb);
+    load(b1, st1, qb, sb);
     consume(b, st, qa, sa);
     b = b1;
     st = st1;
@@ -211,7 +221,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const float* __restric
     b1 = b;
     st1 = st + 1;
     if (st1 == nsteps) { st1 = 0; b1 += GW; }
-    if (b1 < nblk) load(b1, st1, qa, sa);
+    load(b1, st1, qa, sa);
     consume(b, st, qb, sb);
     b = b1;
     st = st1;
@@ -288,11 +298,24 @@ hipError_t launch_stream_t(const float* x, const int8_t* w, const float* s, floa
                            int gs, hipStream_t st) {
   auto kern = stream_kernel<R, U, MT, GS>;
   const size_t lds = static_cast<size_t>(MT) * K * sizeof(float);
-  // Resident workgroups per CU for this kernel: its register use allows 7-8; 8 is enough to keep
-  // two steps of loads in flight per wave.
-  constexpr int kWgPerCu = 8;
+  // Persistent grid: exactly as many workgroups as can be resident at once (the occupancy
+  // calculator's answer for this kernel and LDS size, cached per device and LDS size).
+  static int cached_dev = -1;
+  static size_t cached_lds = 0;
+  static int cached_blocks = 0;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  if (dev != cached_dev || lds != cached_lds) {
+    int blocks = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, kThreads, lds) != hipSuccess ||
+        blocks <= 0)
+      blocks = 4;
+    cached_dev = dev;
+    cached_lds = lds;
+    cached_blocks = blocks;
+  }
   const int nblk = (N + R - 1) / R;
-  const int grid = min((nblk + kWaves - 1) / kWaves, cu_count() * kWgPerCu);
+  const int grid = min((nblk + kWaves - 1) / kWaves, cu_count() * cached_blocks);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, st, x, w, s, y, N, K, gs);
   return hipGetLastError();
 }

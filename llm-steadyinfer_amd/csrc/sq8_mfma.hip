@@ -428,11 +428,12 @@ __global__ __launch_bounds__(kThreads) void skinny16_kernel(
           p = __builtin_amdgcn_mfma_f32_16x16x32_f16(al0, bw[j][0], p, 0, 0, 0);
           p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah1, bw[j][1], p, 0, 0, 0);
           p = __builtin_amdgcn_mfma_f32_16x16x32_f16(al1, bw[j][1], p, 0, 0, 0);
+          // (scale * partial) * 2^-e: the product scale * 2^-e alone can underflow for tiny rows.
           const float sc = wsc[b][q][j];
-          acc[i][j][0] = fmaf(sc * rs.x, p[0], acc[i][j][0]);
-          acc[i][j][1] = fmaf(sc * rs.y, p[1], acc[i][j][1]);
-          acc[i][j][2] = fmaf(sc * rs.z, p[2], acc[i][j][2]);
-          acc[i][j][3] = fmaf(sc * rs.w, p[3], acc[i][j][3]);
+          acc[i][j][0] = fmaf(sc * p[0], rs.x, acc[i][j][0]);
+          acc[i][j][1] = fmaf(sc * p[1], rs.y, acc[i][j][1]);
+          acc[i][j][2] = fmaf(sc * p[2], rs.z, acc[i][j][2]);
+          acc[i][j][3] = fmaf(sc * p[3], rs.w, acc[i][j][3]);
         }
       }
     }
@@ -494,6 +495,216 @@ __global__ __launch_bounds__(kThreads) void skinny16_kernel(
     }
   // Wait until this thread's partial stores are acknowledged (s_waitcnt with every counter at
   // zero) before the workgroup takes its ticket.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0)
+    is_last = __hip_atomic_fetch_add(&tickets[blockIdx.x], 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) == static_cast<unsigned>(splits - 1);
+  __syncthreads();
+  if (!is_last) return;
+  const int ncols = min(BN, N - n0);
+  for (int idx = tid; idx < M * ncols; idx += kThreads) {
+    const int m = idx / ncols, nn = n0 + idx % ncols;
+    const size_t o = static_cast<size_t>(m) * N + nn;
+    float v = __hip_atomic_load(part + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int z = 1; z < splits; ++z)
+      v += __hip_atomic_load(part + static_cast<size_t>(z) * M * N + o, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    y[o] = v;
+  }
+  if (tid == 0)
+    __hip_atomic_store(&tickets[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------- int8-limb decode kernel
+// For 1 <= M <= 4*NB token rows on v_mfma_i32_16x16x64_i8, with the int8 weights as the B operand
+// exactly as they sit in memory (no conversion at all). Each activation row t is split per 64-wide
+// group g into a power of two and four signed 7-bit limbs:
+//     round(x * 2^e) = ((a0*128 + a1)*128 + a2)*128 + a3,  |round(x * 2^e)| < 2^27, |aj| <= 64
+// where 2^e puts the row's group absmax in [2^25, 2^26): 27 significant bits per element relative
+// to its group's absmax. Rows 4t+j of the A operand hold limb j of token t, so one MFMA gives, in
+// int32 and exactly, the four limb dot products of up to 4 tokens against 16 output columns over a
+// whole group; each lane then combines the four sums of its (token, column) in fp32 and adds
+// scale[n, g] * 2^-e * sum. Everything else (chunked double-buffered weight registers, activation
+// limbs staged once per workgroup in LDS, fence-free split-K) is as in the f16 skinny kernel.
+//  * lane l, weight tile j: row n0 + 16j + l%16, bytes (l/16)*16 .. +16 of each group (B operand);
+//  * A operand: row l%16 (token (l%16)/4, limb l%4), the same 16 k positions, from LDS;
+//  * result lane l: column l%16, rows 4*(l/16) + i = limbs i of token l/16 (in row block b).
+typedef int i32x4v __attribute__((ext_vector_type(4)));
+constexpr int kLimbRowBytes = 80;  // 64 limb bytes + 16 padding: conflict-free ds_read_b128
+
+template <int NB, int KW, int TN>
+__global__ __launch_bounds__(kThreads) void skinny_i8_kernel(
+    const float* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ s,
+    float* __restrict__ y, float* __restrict__ part, unsigned* __restrict__ tickets, int M, int N,
+    int K, int gs, int gps, int splits) {
+  constexpr int MT = 4 * NB;                       // token slots
+  constexpr int ROWS = 16 * NB;                    // A rows (4 limbs per token)
+  constexpr int BN = 4 * TN * 16;                  // 4 waves x TN tiles of 16 columns
+  constexpr int GROUP_BYTES = ROWS * kLimbRowBytes;
+  // Activation staging: one thread per (token, group, 4 consecutive k).
+  constexpr int XJOBS = MT * KW * 16;
+  constexpr int XPT = (XJOBS + kThreads - 1) / kThreads;
+  __shared__ __attribute__((aligned(16))) int8_t sa[2][KW * GROUP_BYTES];
+  __shared__ __attribute__((aligned(16))) float sx2[2][KW * MT];  // 2^-e per (group, token)
+  __shared__ int is_last;
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int lcol = lane & 15, kq = (lane >> 4) * 16;
+  const int n0 = blockIdx.x * BN;
+  const int gbeg = blockIdx.y * gps;
+  const int nch = (min(K / BK, gbeg + gps) - gbeg) / KW;
+  const int gpr = K / gs;
+
+  const int8_t* wsrc[TN];
+  const float* ssrc[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int ncol = min(n0 + (wave * TN + j) * 16 + lcol, N - 1);
+    wsrc[j] = w + static_cast<size_t>(ncol) * K + static_cast<size_t>(gbeg) * BK + kq;
+    ssrc[j] = s + static_cast<size_t>(ncol) * gpr;
+  }
+
+  i32x4v wr[2][KW][TN];
+  float wsc[2][KW][TN];
+  auto wload = [&](int b, int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < KW; ++q)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        wr[b][q][j] = __builtin_nontemporal_load(
+            reinterpret_cast<const i32x4v*>(wsrc[j] + (c * KW + q) * BK));
+        wsc[b][q][j] = ssrc[j][((gbeg + c * KW + q) * BK) / gs];
+      }
+  };
+  float4 xr[XPT];
+  auto xload = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int f = min(tid + kThreads * i, XJOBS - 1);
+      const int t = f / (KW * 16), rem = f % (KW * 16);
+      xr[i] = *reinterpret_cast<const float4*>(x + static_cast<size_t>(min(t, M - 1)) * K +
+                                               (gbeg + c * KW) * BK + rem * 4);
+    }
+  };
+  auto xstore = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int f = tid + kThreads * i;
+      const bool job = f < XJOBS;
+      const int fc = min(f, XJOBS - 1);
+      const int t = fc / (KW * 16), rem = fc % (KW * 16), q = rem >> 4, part4 = rem & 15;
+      const float4 v = (job && t < M) ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+      for (int off = 8; off >= 1; off /= 2) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+      int e = 0;
+      if (amax > 0.f && amax <= 3.402823466e38f) {
+        int ex;
+        frexpf(amax, &ex);
+        e = min(max(26 - ex, -126), 126);
+      }
+      const float xf[4] = {v.x, v.y, v.z, v.w};
+      uint32_t limb[4] = {0u, 0u, 0u, 0u};  // limb j of the 4 elements, one byte each
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        int X = static_cast<int>(rintf(ldexpf(xf[c], e)));
+#pragma unroll
+        for (int j = 3; j >= 1; --j) {
+          const int a = ((X + 64) & 127) - 64;
+          limb[j] |= (static_cast<uint32_t>(a) & 0xffu) << (8 * c);
+          X = (X - a) >> 7;
+        }
+        limb[0] |= (static_cast<uint32_t>(X) & 0xffu) << (8 * c);
+      }
+      if (job) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<uint32_t*>(&sa[b][q * GROUP_BYTES + (4 * t + j) * kLimbRowBytes +
+                                            part4 * 4]) = limb[j];
+        if (part4 == 0) sx2[b][q * MT + t] = ldexpf(1.f, -e);
+      }
+    }
+  };
+
+  float acc[NB][TN];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[b][j] = 0.f;
+  auto compute = [&](int bb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < KW; ++q) {
+#pragma unroll
+      for (int rb = 0; rb < NB; ++rb) {
+        const i32x4v a = *reinterpret_cast<const i32x4v*>(
+            &sa[bb][q * GROUP_BYTES + (rb * 16 + lcol) * kLimbRowBytes + kq]);
+        const float r2 = sx2[bb][q * MT + rb * 4 + (lane >> 4)];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const i32x4v zero = {0, 0, 0, 0};
+          const i32x4v d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, wr[bb][q][j], zero, 0, 0, 0);
+          // ((c0*128 + c1)*128 + c2)*128 + c3 = sum of round(x * 2^e) * q; times scale * 2^-e
+          float v = static_cast<float>(d[0]);
+          v = fmaf(v, 128.f, static_cast<float>(d[1]));
+          v = fmaf(v, 128.f, static_cast<float>(d[2]));
+          v = fmaf(v, 128.f, static_cast<float>(d[3]));
+          // scale * v is the partial for activations normalised to [2^25, 2^26): in range for any
+          // finite weight scale. Folding 2^-e into the scale first would underflow for tiny rows.
+          acc[rb][j] = fmaf(wsc[bb][q][j] * v, r2, acc[rb][j]);
+        }
+      }
+    }
+  };
+
+  // Zero both LDS buffers once: token slots >= M stay zero.
+  for (int i = tid * 4; i < 2 * KW * GROUP_BYTES; i += kThreads * 4)
+    *reinterpret_cast<uint32_t*>(&sa[0][0] + i) = 0u;
+  __syncthreads();
+  if (nch > 0) {
+    xload(0);
+    wload(0, 0);
+    xstore(0);
+  }
+  __syncthreads();
+  auto step = [&](auto buf, int c) __attribute__((always_inline)) {
+    constexpr int B = decltype(buf)::value;
+    const bool more = c + 1 < nch;
+    if (more) xload(c + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (more) wload(B ^ 1, c + 1);
+    compute(B);
+    if (more) xstore(B ^ 1);
+    __syncthreads();
+  };
+  for (int c = 0; c < nch;) {
+    step(std::integral_constant<int, 0>{}, c);
+    if (++c >= nch) break;
+    step(std::integral_constant<int, 1>{}, c);
+    ++c;
+  }
+
+  // Lane l holds token 4*rb + l/16 of column (tile) + l%16.
+  if (splits == 1) {
+#pragma unroll
+    for (int rb = 0; rb < NB; ++rb)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int m = rb * 4 + (lane >> 4), n = n0 + (wave * TN + j) * 16 + lcol;
+        if (m < M && n < N) y[static_cast<size_t>(m) * N + n] = acc[rb][j];
+      }
+    return;
+  }
+  float* dst = part + static_cast<size_t>(blockIdx.y) * M * N;
+#pragma unroll
+  for (int rb = 0; rb < NB; ++rb)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int m = rb * 4 + (lane >> 4), n = n0 + (wave * TN + j) * 16 + lcol;
+      if (m < M && n < N)
+        __hip_atomic_store(dst + static_cast<size_t>(m) * N + n, acc[rb][j], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0)
@@ -605,6 +816,16 @@ hipError_t launch_skinny16(const float* x, const int8_t* w, const float* s, floa
   return hipGetLastError();
 }
 
+template <int NB, int KW, int TN>
+hipError_t launch_skinny_i8(const float* x, const int8_t* w, const float* s, float* y, float* part,
+                            unsigned* tickets, int M, int N, int K, int gs, const Plan& p,
+                            hipStream_t st) {
+  const dim3 grid((N + 64 * TN - 1) / (64 * TN), p.splits);
+  hipLaunchKernelGGL((skinny_i8_kernel<NB, KW, TN>), grid, dim3(kThreads), 0, st, x, w, s, y,
+                     part, tickets, M, N, K, gs, p.groups_per_split, p.splits);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 // Workspace layout: [ticket array, kTicketBytes][path buffers]. The ticket array must be zero
@@ -635,6 +856,11 @@ hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y
     case 2: return launch_skinny16<MR, 2, 1, MT16>(x, w, s, y, part, tickets, M, N, K, gs, p, st); \
     default: return launch_skinny16<MR, 1, 1, MT16>(x, w, s, y, part, tickets, M, N, K, gs, p, st); \
   }
+    if (M <= 4) {  // int8-limb MFMA kernel: one MFMA covers 4 tokens
+      if (p.kw == 4) return launch_skinny_i8<1, 4, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st);
+      if (p.kw == 2) return launch_skinny_i8<1, 2, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st);
+      return launch_skinny_i8<1, 1, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st);
+    }
     if (M <= 8 && p.kw == 4)
       return launch_skinny16<8, 4, 1, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st);
     if (M <= 8 && p.kw == 2)
