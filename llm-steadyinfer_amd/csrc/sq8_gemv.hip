@@ -4,12 +4,16 @@
 // 128-thread block per output row with 1-byte scalar weight loads, a per-element scale gather and
 // a cub block reduction per (row, token).
 //
-// Two kernels:
-//  - stream_kernel (M <= 2, the decode GEMV): persistent waves; each wave owns blocks of R output
-//    rows and streams them in steps of U KiB per row, with the next step's weight loads issued
-//    before the current step is consumed (two register sets), so a wave always has loads in flight.
-//    The token rows are staged once per workgroup in LDS. Each lane converts its 16 int8 per row
-//    with SDWA byte-select conversions and applies the group scale once per 16-element chunk.
+// Three kernels:
+//  - sweep_kernel (M <= 2, rows shorter than 8 KiB: QKV, O, gate/up, LM head of Llama-3-8B): the
+//    token rows are staged once per workgroup in LDS; each wave takes row blocks of R rows in grid
+//    stride and walks K in steps of U KiB per row. Latency is hidden by residency (16 waves per CU)
+//    and by the compiler's interleaving of a step's loads with its dot products; only the group
+//    scales are fetched a step ahead. Each lane converts its 16 int8 per row with SDWA byte-select
+//    conversions and applies the group scale once per 16-element chunk.
+//  - stream_kernel (M <= 2, rows of 8 KiB and more: the down projection): persistent waves with
+//    two register sets, so the next step's weight loads are in flight while the current step is
+//    consumed.
 //  - gemv_rows_kernel (fallback for larger M or K beyond the LDS budget):
 // a 256-thread workgroup (4 wave64s) owns R consecutive output rows and the whole K
 // extent. Every lane streams 16 int8 weights per row per step with one dwordx4 load; the 256 lanes
@@ -61,7 +65,7 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const float* __rest
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
   const int n0 = blockIdx.x * R;
   const int gs = GS ? GS : gs_rt;
   const int chunks_per_group = gs >> 4;
@@ -137,7 +141,7 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const float* __restric
                                                           float* __restrict__ y, int N, int K,
                                                           int gs_rt) {
   extern __shared__ float xs[];
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
   const int nblk = (N + R - 1) / R;
   const int GW = gridDim.x * kWaves;
   const int gw = blockIdx.x * kWaves + wave;
@@ -223,6 +227,101 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const float* __restric
     if (st1 == nsteps) { st1 = 0; b1 += GW; }
     load(b1, st1, qa, sa);
     consume(b, st, qb, sb);
+    b = b1;
+    st = st1;
+  }
+}
+
+// Decode GEMV for rows shorter than 8 KiB. MT token rows (MT = M <= 2) are staged in LDS once per
+// workgroup; wave w of the grid takes row blocks w, w + GW, ... of R rows and walks K in steps of
+// U KiB per row, issuing all R x U dwordx4 loads of a step before using any of them. Latency is
+// hidden by residency (four 4-wave workgroups per CU) rather than by a second register set, which
+// keeps the register count low enough for that residency. TAIL: K is not a multiple of U KiB.
+template <int R, int U, int MT, int GS, bool TAIL>
+__global__ __launch_bounds__(kThreads) void sweep_kernel(const float* __restrict__ x,
+                                                         const int8_t* __restrict__ w,
+                                                         const float* __restrict__ s,
+                                                         float* __restrict__ y, int N, int K,
+                                                         int gs_rt) {
+  extern __shared__ float xs[];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
+  // float4 number i is stored at i ^ ((i >> 4) & 3) (see stream_kernel).
+  for (int i = tid; i < MT * K / 4; i += kThreads)
+    reinterpret_cast<float4*>(xs)[i ^ ((i >> 4) & 3)] = reinterpret_cast<const float4*>(x)[i];
+  __syncthreads();
+  const int nblk = (N + R - 1) / R;
+  const int GW = gridDim.x * kWaves;
+  const int gs = GS ? GS : gs_rt;
+  const int gpr = K / gs;
+  const int nsteps = (K + 1024 * U - 1) / (1024 * U);
+  // The scales of a step are loaded one step ahead. Needed only after the dot products, they would
+  // otherwise be scheduled after them and add a second memory round trip to every step. Rows
+  // past N (including those of a block past the last) are clamped to row N - 1.
+  auto load_scales = [&](int b, int st, float (&sc)[U][R]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = (st * U + u) * 1024 + lane * 16;
+      const int kc = !TAIL || k < K ? k : 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        sc[u][r] = s[static_cast<size_t>(min(b * R + r, N - 1)) * gpr + kc / gs];
+    }
+  };
+  float acc[R * MT];
+#pragma unroll
+  for (int i = 0; i < R * MT; ++i) acc[i] = 0.f;
+  int b = blockIdx.x * kWaves + wave, st = 0;
+  float scn[U][R];
+  load_scales(b, st, scn);
+  while (b < nblk) {
+    i32x4 q[U][R];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = (st * U + u) * 1024 + lane * 16;
+      const bool ok = !TAIL || k < K;
+      const int kc = ok ? k : 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int n = min(b * R + r, N - 1);
+        const i32x4 v = __builtin_nontemporal_load(
+            reinterpret_cast<const i32x4*>(w + static_cast<size_t>(n) * K + kc));
+        q[u][r] = ok ? v : i32x4{0, 0, 0, 0};
+      }
+    }
+    float sc[U][R];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int r = 0; r < R; ++r) sc[u][r] = scn[u][r];
+    int b1 = b, st1 = st + 1;
+    if (st1 == nsteps) { st1 = 0; b1 += GW; }
+    load_scales(b1, st1, scn);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = (st * U + u) * 1024 + lane * 16;
+      const int kc = !TAIL || k < K ? k : 0;
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const int i0 = (t * K + kc) / 4;
+        const float4* xp = reinterpret_cast<const float4*>(xs) + i0;
+        const int sw = (i0 >> 4) & 3;
+        const float4 x0 = xp[0 ^ sw], x1 = xp[1 ^ sw], x2 = xp[2 ^ sw], x3 = xp[3 ^ sw];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          acc[r * MT + t] = fmaf(sc[u][r], dot16(q[u][r], x0, x1, x2, x3), acc[r * MT + t]);
+      }
+    }
+    if (st == nsteps - 1) {
+      wave_reduce_scatter<R * MT>(acc, lane);
+      constexpr int kSpan = kWave / (R * MT);
+      if ((lane & (kSpan - 1)) == 0) {
+        const int idx = lane / kSpan, r = idx / MT, t = idx % MT;
+        const int n = b * R + r;
+        if (n < N) y[static_cast<size_t>(t) * N + n] = acc[0];
+      }
+#pragma unroll
+      for (int i = 0; i < R * MT; ++i) acc[i] = 0.f;
+    }
     b = b1;
     st = st1;
   }
@@ -320,16 +419,34 @@ hipError_t launch_stream_t(const float* x, const int8_t* w, const float* s, floa
   return hipGetLastError();
 }
 
+// Four workgroups per CU (16 waves), fewer when there are fewer row blocks than waves.
+template <int R, int U, int MT, int GS>
+hipError_t launch_sweep_t(const float* x, const int8_t* w, const float* s, float* y, int N, int K,
+                          int gs, hipStream_t st) {
+  const size_t lds = static_cast<size_t>(MT) * K * sizeof(float);
+  const int nblk = (N + R - 1) / R;
+  const int grid = min((nblk + kWaves - 1) / kWaves, 4 * cu_count());
+  if (K % (1024 * U) == 0) {
+    hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, false>), dim3(grid), dim3(kThreads), lds, st, x,
+                       w, s, y, N, K, gs);
+  } else {
+    hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, true>), dim3(grid), dim3(kThreads), lds, st, x,
+                       w, s, y, N, K, gs);
+  }
+  return hipGetLastError();
+}
+
 template <int MT>
 hipError_t launch_stream(const float* x, const int8_t* w, const float* s, float* y, int N, int K,
                          int gs, hipStream_t st) {
-  // Long rows (K >= 8 KiB): two 1 KiB iterations per step; short rows: four.
+  // Long rows (K >= 8 KiB): persistent prefetching stream, two 1 KiB iterations per step.
+  // Shorter rows: the residency-hidden sweep, four 1 KiB iterations per step.
   if (K >= 8192) {
     return gs == 64 ? launch_stream_t<2, 2, MT, 64>(x, w, s, y, N, K, gs, st)
                     : launch_stream_t<2, 2, MT, 0>(x, w, s, y, N, K, gs, st);
   }
-  return gs == 64 ? launch_stream_t<2, 4, MT, 64>(x, w, s, y, N, K, gs, st)
-                  : launch_stream_t<2, 4, MT, 0>(x, w, s, y, N, K, gs, st);
+  return gs == 64 ? launch_sweep_t<2, 4, MT, 64>(x, w, s, y, N, K, gs, st)
+                  : launch_sweep_t<2, 4, MT, 0>(x, w, s, y, N, K, gs, st);
 }
 
 }  // namespace

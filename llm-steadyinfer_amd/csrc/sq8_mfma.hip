@@ -112,7 +112,7 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
     float* __restrict__ out, int M, int N, int K, int gs, int groups_per_split) {
   using T = Tile<WAVES_M, WAVES_N, TM, TN>;
   extern __shared__ _Float16 lds[];
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int n0 = blockIdx.x * T::BN, m0 = blockIdx.y * T::BM;
   const int nsteps = K / BK;
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(kThreads) void skinny16_kernel(
   __shared__ __attribute__((aligned(16))) float sxs[2][KW * BMP];
   __shared__ int is_last;
 
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
   const int lcol = lane & 15, kq = (lane >> 4) * 16;
   const int n0 = blockIdx.x * BN;
   const int gbeg = blockIdx.y * gps;
@@ -549,7 +549,7 @@ __global__ __launch_bounds__(kThreads) void skinny_i8_kernel(
   __shared__ __attribute__((aligned(16))) float sx2[2][KW * MT];  // 2^-e per (group, token)
   __shared__ int is_last;
 
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
   const int lcol = lane & 15, kq = (lane >> 4) * 16;
   const int n0 = blockIdx.x * BN;
   const int gbeg = blockIdx.y * gps;
