@@ -4,16 +4,13 @@
 // 128-thread block per output row with 1-byte scalar weight loads, a per-element scale gather and
 // a cub block reduction per (row, token).
 //
-// Three kernels:
-//  - sweep_kernel (M <= 2, rows shorter than 8 KiB: QKV, O, gate/up, LM head of Llama-3-8B): the
-//    token rows are staged once per workgroup in LDS; each wave takes row blocks of R rows in grid
-//    stride and walks K in steps of U KiB per row. Latency is hidden by residency (16 waves per CU)
-//    and by the compiler's interleaving of a step's loads with its dot products; only the group
-//    scales are fetched a step ahead. Each lane converts its 16 int8 per row with SDWA byte-select
-//    conversions and applies the group scale once per 16-element chunk.
-//  - stream_kernel (M <= 2, rows of 8 KiB and more: the down projection): persistent waves with
-//    two register sets, so the next step's weight loads are in flight while the current step is
-//    consumed.
+// Two kernels:
+//  - sweep_kernel (M <= 2, the decode GEMV): the token rows are staged once per workgroup in
+//    LDS; each wave takes row blocks of R rows in grid stride and walks K in steps of U KiB per
+//    row. Latency is hidden by residency (up to 16 waves per CU) and by the compiler's
+//    interleaving of a step's loads with its dot products; only the group scales are fetched a
+//    step ahead. Each lane converts its 16 int8 per row with SDWA byte-select conversions and
+//    applies the group scale once per 16-element chunk.
 //  - gemv_rows_kernel (fallback for larger M or K beyond the LDS budget):
 // a 256-thread workgroup (4 wave64s) owns R consecutive output rows and the whole K
 // extent. Every lane streams 16 int8 weights per row per step with one dwordx4 load; the 256 lanes
@@ -132,125 +129,27 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const float* __rest
   }
 }
 
-// Persistent decode GEMV. MT token rows (MT = M <= 2) are staged in LDS; wave w of the grid owns
-// row blocks w, w + GW, ... of R rows. A step is U iterations of 1 KiB per row (64 lanes x 16 B).
-template <int R, int U, int MT, int GS>
-__global__ __launch_bounds__(kThreads) void stream_kernel(const float* __restrict__ x,
-                                                          const int8_t* __restrict__ w,
-                                                          const float* __restrict__ s,
-                                                          float* __restrict__ y, int N, int K,
-                                                          int gs_rt) {
-  extern __shared__ float xs[];
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
-  const int nblk = (N + R - 1) / R;
-  const int GW = gridDim.x * kWaves;
-  const int gw = blockIdx.x * kWaves + wave;
-  const int its = (K + 1023) >> 10;
-  const int nsteps = (its + U - 1) / U;  // steps per row block
-  const int gs = GS ? GS : gs_rt;
-  const int gpr = K / gs;
-
-  i32x4 qa[U][R], qb[U][R];
-  float sa[U][R], sb[U][R];
-  // Loads are issued unconditionally (a step past the last block reads the first bytes of x, which
-  // are cached, and is never consumed): with no branch around them the compiler's wait counts stay
-  // exact, so waiting for one step never drains the prefetch of the next.
-  auto load = [&](int b, int st, i32x4 (&q)[U][R], float (&sc)[U][R]) __attribute__((always_inline)) {
-    const bool live = b < nblk;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = (st * U + u) * 1024 + lane * 16;
-      const bool ok = k < K;
-      const int kc = ok ? k : 0;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int n = min(b * R + r, N - 1);
-        const i32x4* wp = live ? reinterpret_cast<const i32x4*>(w + static_cast<size_t>(n) * K + kc)
-                               : reinterpret_cast<const i32x4*>(x);
-        const float* sp = live ? s + static_cast<size_t>(n) * gpr + kc / gs : x;
-        const i32x4 v = __builtin_nontemporal_load(wp);
-        q[u][r] = ok ? v : i32x4{0, 0, 0, 0};
-        sc[u][r] = *sp;
-      }
-    }
-  };
-  float acc[R * MT];
-#pragma unroll
-  for (int i = 0; i < R * MT; ++i) acc[i] = 0.f;
-  auto consume = [&](int b, int st, const i32x4 (&q)[U][R], const float (&sc)[U][R]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = (st * U + u) * 1024 + lane * 16;
-      const int kc = k < K ? k : 0;
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const int i0 = (t * K + kc) / 4;  // float4 number of the chunk's first 4 elements
-        const float4* xp = reinterpret_cast<const float4*>(xs) + i0;
-        const int sw = (i0 >> 4) & 3;      // the staging swizzle of float4 numbers i0 .. i0+3
-        const float4 x0 = xp[0 ^ sw], x1 = xp[1 ^ sw], x2 = xp[2 ^ sw], x3 = xp[3 ^ sw];
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-          acc[r * MT + t] = fmaf(sc[u][r], dot16(q[u][r], x0, x1, x2, x3), acc[r * MT + t]);
-      }
-    }
-    if (st == nsteps - 1) {
-      wave_reduce_scatter<R * MT>(acc, lane);
-      constexpr int kSpan = kWave / (R * MT);
-      if ((lane & (kSpan - 1)) == 0) {
-        const int idx = lane / kSpan, r = idx / MT, t = idx % MT;
-        const int n = b * R + r;
-        if (n < N) y[static_cast<size_t>(t) * N + n] = acc[0];
-      }
-#pragma unroll
-      for (int i = 0; i < R * MT; ++i) acc[i] = 0.f;
-    }
-  };
-
-  int b = gw, st = 0;
-  load(b, st, qa, sa);
-  // Stage x after the first weight loads are in flight. float4 number i is stored at
-  // i ^ ((i >> 4) & 3): a lane reads the 4 float4 of its 16-element chunk, and without the swizzle
-  // lanes l and l+4 would hit the same LDS banks in every ds_read_b128 (4-way conflicts).
-  for (int i = tid; i < MT * K / 4; i += kThreads)
-    reinterpret_cast<float4*>(xs)[i ^ ((i >> 4) & 3)] = reinterpret_cast<const float4*>(x)[i];
-  __syncthreads();
-  while (b < nblk) {
-    int b1 = b, st1 = st + 1;
-    if (st1 == nsteps) { st1 = 0; b1 += GW; }
-    load(b1, st1, qb, sb);
-    consume(b, st, qa, sa);
-    b = b1;
-    st = st1;
-    if (b >= nblk) break;
-    b1 = b;
-    st1 = st + 1;
-    if (st1 == nsteps) { st1 = 0; b1 += GW; }
-    load(b1, st1, qa, sa);
-    consume(b, st, qb, sb);
-    b = b1;
-    st = st1;
-  }
-}
-
-// Decode GEMV for rows shorter than 8 KiB. MT token rows (MT = M <= 2) are staged in LDS once per
+// Decode GEMV. MT token rows (MT = M <= 2) are staged in LDS once per
 // workgroup; wave w of the grid takes row blocks w, w + GW, ... of R rows and walks K in steps of
 // U KiB per row, issuing all R x U dwordx4 loads of a step before using any of them. Latency is
 // hidden by residency (four 4-wave workgroups per CU) rather than by a second register set, which
 // keeps the register count low enough for that residency. TAIL: K is not a multiple of U KiB.
-template <int R, int U, int MT, int GS, bool TAIL>
-__global__ __launch_bounds__(kThreads) void sweep_kernel(const float* __restrict__ x,
+template <int R, int U, int MT, int GS, bool TAIL, int WV = kWaves>
+__global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restrict__ x,
                                                          const int8_t* __restrict__ w,
                                                          const float* __restrict__ s,
                                                          float* __restrict__ y, int N, int K,
                                                          int gs_rt) {
   extern __shared__ float xs[];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
-  // float4 number i is stored at i ^ ((i >> 4) & 3) (see stream_kernel).
-  for (int i = tid; i < MT * K / 4; i += kThreads)
+  // float4 number i is stored at i ^ ((i >> 4) & 3): a lane reads the 4 float4 of its 16-element
+  // chunk, and without the swizzle lanes l and l+4 would hit the same LDS banks in every
+  // ds_read_b128 (4-way conflicts).
+  for (int i = tid; i < MT * K / 4; i += WV * kWave)
     reinterpret_cast<float4*>(xs)[i ^ ((i >> 4) & 3)] = reinterpret_cast<const float4*>(x)[i];
   __syncthreads();
   const int nblk = (N + R - 1) / R;
-  const int GW = gridDim.x * kWaves;
+  const int GW = gridDim.x * WV;
   const int gs = GS ? GS : gs_rt;
   const int gpr = K / gs;
   const int nsteps = (K + 1024 * U - 1) / (1024 * U);
@@ -270,7 +169,7 @@ __global__ __launch_bounds__(kThreads) void sweep_kernel(const float* __restrict
   float acc[R * MT];
 #pragma unroll
   for (int i = 0; i < R * MT; ++i) acc[i] = 0.f;
-  int b = blockIdx.x * kWaves + wave, st = 0;
+  int b = blockIdx.x * WV + wave, st = 0;
   float scn[U][R];
   load_scales(b, st, scn);
   while (b < nblk) {
@@ -392,33 +291,6 @@ namespace {
 // LDS bytes the stream kernel may use for staged token rows (MT * K fp32).
 constexpr size_t kStreamLdsMax = 64 * 1024;
 
-template <int R, int U, int MT, int GS>
-hipError_t launch_stream_t(const float* x, const int8_t* w, const float* s, float* y, int N, int K,
-                           int gs, hipStream_t st) {
-  auto kern = stream_kernel<R, U, MT, GS>;
-  const size_t lds = static_cast<size_t>(MT) * K * sizeof(float);
-  // Persistent grid: exactly as many workgroups as can be resident at once (the occupancy
-  // calculator's answer for this kernel and LDS size, cached per device and LDS size).
-  static int cached_dev = -1;
-  static size_t cached_lds = 0;
-  static int cached_blocks = 0;
-  int dev = 0;
-  (void)hipGetDevice(&dev);
-  if (dev != cached_dev || lds != cached_lds) {
-    int blocks = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kern, kThreads, lds) != hipSuccess ||
-        blocks <= 0)
-      blocks = 4;
-    cached_dev = dev;
-    cached_lds = lds;
-    cached_blocks = blocks;
-  }
-  const int nblk = (N + R - 1) / R;
-  const int grid = min((nblk + kWaves - 1) / kWaves, cu_count() * cached_blocks);
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(kThreads), lds, st, x, w, s, y, N, K, gs);
-  return hipGetLastError();
-}
-
 // Four workgroups per CU (16 waves), fewer when there are fewer row blocks than waves.
 template <int R, int U, int MT, int GS>
 hipError_t launch_sweep_t(const float* x, const int8_t* w, const float* s, float* y, int N, int K,
@@ -439,11 +311,11 @@ hipError_t launch_sweep_t(const float* x, const int8_t* w, const float* s, float
 template <int MT>
 hipError_t launch_stream(const float* x, const int8_t* w, const float* s, float* y, int N, int K,
                          int gs, hipStream_t st) {
-  // Long rows (K >= 8 KiB): persistent prefetching stream, two 1 KiB iterations per step.
-  // Shorter rows: the residency-hidden sweep, four 1 KiB iterations per step.
+  // Four 1 KiB iterations per step for rows under 8 KiB, two for longer rows (measured best on
+  // the Llama-3-8B shapes).
   if (K >= 8192) {
-    return gs == 64 ? launch_stream_t<2, 2, MT, 64>(x, w, s, y, N, K, gs, st)
-                    : launch_stream_t<2, 2, MT, 0>(x, w, s, y, N, K, gs, st);
+    return gs == 64 ? launch_sweep_t<2, 2, MT, 64>(x, w, s, y, N, K, gs, st)
+                    : launch_sweep_t<2, 2, MT, 0>(x, w, s, y, N, K, gs, st);
   }
   return gs == 64 ? launch_sweep_t<2, 4, MT, 64>(x, w, s, y, N, K, gs, st)
                   : launch_sweep_t<2, 4, MT, 0>(x, w, s, y, N, K, gs, st);
