@@ -38,7 +38,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense f16 matrix peak (the prefill GEMM issues f16 MFMA)
 # HBM bytes per M=1 GEMV launch over algorithmic bytes, from rocprofv3 FETCH_SIZE/WRITE_SIZE passes
 # over `python bench.py --profile`, scaled by a 256 MiB copy of known size (profiles/).
-GEMV_TRAFFIC_RATIO = 1.005
+GEMV_TRAFFIC_RATIO = 1.004
 METRIC = "INT8 GEMV HBM GB/s (% of peak) + decode tokens/s, Llama-3-8B shapes, 1 GPU"
 
 
@@ -227,7 +227,7 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": round(bytes_per_launch * GEMV_TRAFFIC_RATIO),
-                "kernel": "sq8 stream_kernel, M=1 decode GEMV (<2,4,1,64> for K=4096, "
+                "kernel": "sq8 sweep_kernel, M=1 decode GEMV (<2,4,1,64> for K=4096, "
                           "<2,2,1,64> for K=14336)",
                 "avg_launch_us": round(launch_us, 3),
                 "algo_bytes_per_launch": round(bytes_per_launch)}
