@@ -291,34 +291,42 @@ namespace {
 // LDS bytes the stream kernel may use for staged token rows (MT * K fp32).
 constexpr size_t kStreamLdsMax = 64 * 1024;
 
-// Four workgroups per CU (16 waves), fewer when there are fewer row blocks than waves.
-template <int R, int U, int MT, int GS>
+// WV waves per workgroup; 16 waves per CU in total, fewer when there are fewer row blocks.
+template <int R, int U, int MT, int GS, int WV>
 hipError_t launch_sweep_t(const float* x, const int8_t* w, const float* s, float* y, int N, int K,
                           int gs, hipStream_t st) {
   const size_t lds = static_cast<size_t>(MT) * K * sizeof(float);
   const int nblk = (N + R - 1) / R;
-  const int grid = min((nblk + kWaves - 1) / kWaves, 4 * cu_count());
+  const int grid = min((nblk + WV - 1) / WV, (16 / WV) * cu_count());
   if (K % (1024 * U) == 0) {
-    hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, false>), dim3(grid), dim3(kThreads), lds, st, x,
-                       w, s, y, N, K, gs);
+    hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, false, WV>), dim3(grid), dim3(WV * kWave), lds,
+                       st, x, w, s, y, N, K, gs);
   } else {
-    hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, true>), dim3(grid), dim3(kThreads), lds, st, x,
-                       w, s, y, N, K, gs);
+    hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, true, WV>), dim3(grid), dim3(WV * kWave), lds,
+                       st, x, w, s, y, N, K, gs);
   }
   return hipGetLastError();
 }
 
+template <int R, int U, int WV, int MT>
+hipError_t launch_sweep(const float* x, const int8_t* w, const float* s, float* y, int N, int K,
+                        int gs, hipStream_t st) {
+  return gs == 64 ? launch_sweep_t<R, U, MT, 64, WV>(x, w, s, y, N, K, gs, st)
+                  : launch_sweep_t<R, U, MT, 0, WV>(x, w, s, y, N, K, gs, st);
+}
+
+// Configurations measured best on the Llama-3-8B shapes. Rows under 8 KiB: 2 rows per wave,
+// 4 KiB per row per step, four 4-wave workgroups per CU. Longer rows: x fills up to 56 KiB of
+// LDS, so one 16-wave workgroup per CU, one row per wave and 7 KiB (or 2 KiB) per step keep
+// enough bytes in flight.
 template <int MT>
 hipError_t launch_stream(const float* x, const int8_t* w, const float* s, float* y, int N, int K,
                          int gs, hipStream_t st) {
-  // Four 1 KiB iterations per step for rows under 8 KiB, two for longer rows (measured best on
-  // the Llama-3-8B shapes).
   if (K >= 8192) {
-    return gs == 64 ? launch_sweep_t<2, 2, MT, 64>(x, w, s, y, N, K, gs, st)
-                    : launch_sweep_t<2, 2, MT, 0>(x, w, s, y, N, K, gs, st);
+    return K % 7168 == 0 ? launch_sweep<1, 7, 16, MT>(x, w, s, y, N, K, gs, st)
+                         : launch_sweep<1, 2, 16, MT>(x, w, s, y, N, K, gs, st);
   }
-  return gs == 64 ? launch_sweep_t<2, 4, MT, 64>(x, w, s, y, N, K, gs, st)
-                  : launch_sweep_t<2, 4, MT, 0>(x, w, s, y, N, K, gs, st);
+  return launch_sweep<2, 4, 4, MT>(x, w, s, y, N, K, gs, st);
 }
 
 }  // namespace

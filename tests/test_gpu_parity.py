@@ -52,6 +52,17 @@ def test_small_shapes(sq8, dev, M, N, K):
     check(run(sq8, dev, x, q, s, 64), o.matmul_f64(x, q, s, 64), f"M={M} N={N} K={K}")
 
 
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("N,K,gs", [(33, 8192, 64), (50, 9280, 64), (17, 14336, 64),
+                                    (9, 14336, 32), (21, 16000, 64), (300, 7168, 64)])
+def test_long_rows_decode(sq8, dev, M, N, K, gs):
+    """Decode rows of 7-16 K elements: one-row-per-wave configurations, with and without a
+    partial last step, and rows whose staged activations exceed the LDS budget at M=2."""
+    x, q, s = o.make_case(M, N, K, gs, seed=K + N + M)
+    print(f"case M={M} N={N} K={K} gs={gs} path={sq8.path_name(M, N, K, gs)}", flush=True)
+    check(run(sq8, dev, x, q, s, gs), o.matmul_f64(x, q, s, gs), f"M={M} N={N} K={K} gs={gs}")
+
+
 @pytest.mark.parametrize("gs", [16, 32, 128, 256])
 @pytest.mark.parametrize("M", [1, 4, 24, 96])
 def test_other_group_sizes(sq8, dev, gs, M):
