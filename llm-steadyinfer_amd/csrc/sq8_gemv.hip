@@ -315,8 +315,9 @@ hipError_t launch_sweep(const float* x, const int8_t* w, const float* s, float* 
                   : launch_sweep_t<R, U, MT, 0, WV>(x, w, s, y, N, K, gs, st);
 }
 
-// Configurations measured best on the Llama-3-8B shapes. Rows under 8 KiB: 2 rows per wave,
-// 4 KiB per row per step, four 4-wave workgroups per CU. Longer rows: x fills up to 56 KiB of
+// Configurations measured best on the Llama-3-8B shapes. Rows under 8 KiB: 4 KiB per row per
+// step; up to 8192 rows one row per wave in 8-wave workgroups, more rows 2 rows per wave in
+// 4-wave workgroups. Longer rows: x fills up to 56 KiB of
 // LDS, so one 16-wave workgroup per CU, one row per wave and 7 KiB (or 2 KiB) per step keep
 // enough bytes in flight.
 template <int MT>
@@ -326,6 +327,7 @@ hipError_t launch_stream(const float* x, const int8_t* w, const float* s, float*
     return K % 7168 == 0 ? launch_sweep<1, 7, 16, MT>(x, w, s, y, N, K, gs, st)
                          : launch_sweep<1, 2, 16, MT>(x, w, s, y, N, K, gs, st);
   }
+  if (N <= 8192) return launch_sweep<1, 4, 8, MT>(x, w, s, y, N, K, gs, st);
   return launch_sweep<2, 4, 4, MT>(x, w, s, y, N, K, gs, st);
 }
 
