@@ -16,13 +16,13 @@ enum class Path { kGemv, kMfma, kGeneric };
 // group boundary; everything else goes to the exact generic kernel.
 bool fast_shape(int K, int gs) { return gs % 16 == 0 && K % gs == 0; }
 
-// Token rows at which the matrix-core path takes over from the VALU GEMV.
-constexpr int kMfmaMinM = 3;
-
+// Up to 4 token rows whose activations fit the LDS budget go to the VALU GEMV (measured faster
+// than the matrix-core kernels there); everything else with 64-wide groups to the MFMA path.
 Path choose(int M, int N, int K, int gs, bool aligned) {
   (void)N;
   if (!aligned || !fast_shape(K, gs)) return Path::kGeneric;
-  if (M >= kMfmaMinM && gs % 64 == 0) return Path::kMfma;
+  if (sq8::gemv_stream_fits(M, K)) return Path::kGemv;
+  if (M >= 3 && gs % 64 == 0) return Path::kMfma;
   return Path::kGemv;
 }
 

@@ -5,7 +5,7 @@
 // a cub block reduction per (row, token).
 //
 // Two kernels:
-//  - sweep_kernel (M <= 2, the decode GEMV): the token rows are staged once per workgroup in
+//  - sweep_kernel (M <= 4, the decode GEMV): the token rows are staged once per workgroup in
 //    LDS; each wave takes row blocks of R rows in grid stride and walks K in steps of U KiB per
 //    row. Latency is hidden by residency (up to 16 waves per CU) and by the compiler's
 //    interleaving of a step's loads with its dot products; only the group scales are fetched a
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const float* __rest
   }
 }
 
-// Decode GEMV. MT token rows (MT = M <= 2) are staged in LDS once per
+// Decode GEMV. M <= MT token rows (padded with zero rows to MT) are staged in LDS once per
 // workgroup; wave w of the grid takes row blocks w, w + GW, ... of R rows and walks K in steps of
 // U KiB per row, issuing all R x U dwordx4 loads of a step before using any of them. Latency is
 // hidden by residency (four 4-wave workgroups per CU) rather than by a second register set, which
@@ -138,15 +138,19 @@ template <int R, int U, int MT, int GS, bool TAIL, int WV = kWaves>
 __global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restrict__ x,
                                                          const int8_t* __restrict__ w,
                                                          const float* __restrict__ s,
-                                                         float* __restrict__ y, int N, int K,
-                                                         int gs_rt) {
+                                                         float* __restrict__ y, int M, int N,
+                                                         int K, int gs_rt) {
   extern __shared__ float xs[];
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
-  // float4 number i is stored at i ^ ((i >> 4) & 3): a lane reads the 4 float4 of its 16-element
-  // chunk, and without the swizzle lanes l and l+4 would hit the same LDS banks in every
-  // ds_read_b128 (4-way conflicts).
-  for (int i = tid; i < MT * K / 4; i += WV * kWave)
-    reinterpret_cast<float4*>(xs)[i ^ ((i >> 4) & 3)] = reinterpret_cast<const float4*>(x)[i];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
+  // Token rows M .. MT-1 are staged as zeros. float4 number i is stored at i ^ ((i >> 4) & 3): a
+  // lane reads the 4 float4 of its 16-element chunk, and without the swizzle lanes l and l+4 would
+  // hit the same LDS banks in every ds_read_b128 (4-way conflicts).
+  for (int i = tid; i < MT * K / 4; i += WV * kWave) {
+    const float4 v = i < M * K / 4 ? reinterpret_cast<const float4*>(x)[i]
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    reinterpret_cast<float4*>(xs)[i ^ ((i >> 4) & 3)] = v;
+  }
   __syncthreads();
   const int nblk = (N + R - 1) / R;
   const int GW = gridDim.x * WV;
@@ -216,7 +220,7 @@ __global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restri
       if ((lane & (kSpan - 1)) == 0) {
         const int idx = lane / kSpan, r = idx / MT, t = idx % MT;
         const int n = b * R + r;
-        if (n < N) y[static_cast<size_t>(t) * N + n] = acc[0];
+        if (n < N && t < M) y[static_cast<size_t>(t) * N + n] = acc[0];
       }
 #pragma unroll
       for (int i = 0; i < R * MT; ++i) acc[i] = 0.f;
@@ -293,26 +297,26 @@ constexpr size_t kStreamLdsMax = 64 * 1024;
 
 // WV waves per workgroup; 16 waves per CU in total, fewer when there are fewer row blocks.
 template <int R, int U, int MT, int GS, int WV>
-hipError_t launch_sweep_t(const float* x, const int8_t* w, const float* s, float* y, int N, int K,
-                          int gs, hipStream_t st) {
+hipError_t launch_sweep_t(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
+                          int K, int gs, hipStream_t st) {
   const size_t lds = static_cast<size_t>(MT) * K * sizeof(float);
   const int nblk = (N + R - 1) / R;
   const int grid = min((nblk + WV - 1) / WV, (16 / WV) * cu_count());
   if (K % (1024 * U) == 0) {
     hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, false, WV>), dim3(grid), dim3(WV * kWave), lds,
-                       st, x, w, s, y, N, K, gs);
+                       st, x, w, s, y, M, N, K, gs);
   } else {
     hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, true, WV>), dim3(grid), dim3(WV * kWave), lds,
-                       st, x, w, s, y, N, K, gs);
+                       st, x, w, s, y, M, N, K, gs);
   }
   return hipGetLastError();
 }
 
 template <int R, int U, int WV, int MT>
-hipError_t launch_sweep(const float* x, const int8_t* w, const float* s, float* y, int N, int K,
-                        int gs, hipStream_t st) {
-  return gs == 64 ? launch_sweep_t<R, U, MT, 64, WV>(x, w, s, y, N, K, gs, st)
-                  : launch_sweep_t<R, U, MT, 0, WV>(x, w, s, y, N, K, gs, st);
+hipError_t launch_sweep(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
+                        int K, int gs, hipStream_t st) {
+  return gs == 64 ? launch_sweep_t<R, U, MT, 64, WV>(x, w, s, y, M, N, K, gs, st)
+                  : launch_sweep_t<R, U, MT, 0, WV>(x, w, s, y, M, N, K, gs, st);
 }
 
 // Configurations measured best on the Llama-3-8B shapes. Rows under 8 KiB: 4 KiB per row per
@@ -321,28 +325,31 @@ hipError_t launch_sweep(const float* x, const int8_t* w, const float* s, float* 
 // LDS, so one 16-wave workgroup per CU, one row per wave and 7 KiB (or 2 KiB) per step keep
 // enough bytes in flight.
 template <int MT>
-hipError_t launch_stream(const float* x, const int8_t* w, const float* s, float* y, int N, int K,
-                         int gs, hipStream_t st) {
+hipError_t launch_stream(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
+                         int K, int gs, hipStream_t st) {
   if (K >= 8192) {
-    return K % 7168 == 0 ? launch_sweep<1, 7, 16, MT>(x, w, s, y, N, K, gs, st)
-                         : launch_sweep<1, 2, 16, MT>(x, w, s, y, N, K, gs, st);
+    return K % 7168 == 0 ? launch_sweep<1, 7, 16, MT>(x, w, s, y, M, N, K, gs, st)
+                         : launch_sweep<1, 2, 16, MT>(x, w, s, y, M, N, K, gs, st);
   }
-  if (N <= 8192) return launch_sweep<1, 4, 8, MT>(x, w, s, y, N, K, gs, st);
-  return launch_sweep<2, 4, 4, MT>(x, w, s, y, N, K, gs, st);
+  if (N <= 8192) return launch_sweep<1, 4, 8, MT>(x, w, s, y, M, N, K, gs, st);
+  return launch_sweep<2, 4, 4, MT>(x, w, s, y, M, N, K, gs, st);
 }
 
 }  // namespace
 
+// Token rows are staged padded to 1, 2 or 4.
 bool gemv_stream_fits(int M, int K) {
-  return M <= 2 && static_cast<size_t>(M) * K * sizeof(float) <= kStreamLdsMax;
+  const int mt = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
+  return M <= 4 && static_cast<size_t>(mt) * K * sizeof(float) <= kStreamLdsMax;
 }
 
 // Requires: group_size % 16 == 0, K % group_size == 0, 16-byte aligned x and w.
 hipError_t launch_gemv(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
                        int K, int gs, hipStream_t st) {
   if (gemv_stream_fits(M, K)) {
-    return M == 1 ? launch_stream<1>(x, w, s, y, N, K, gs, st)
-                  : launch_stream<2>(x, w, s, y, N, K, gs, st);
+    if (M == 1) return launch_stream<1>(x, w, s, y, M, N, K, gs, st);
+    if (M == 2) return launch_stream<2>(x, w, s, y, M, N, K, gs, st);
+    return launch_sweep<1, 4, 8, 4>(x, w, s, y, M, N, K, gs, st);  // K <= 4096 here
   }
   if (M == 1) return launch_rows<8, 1>(x, w, s, y, M, N, K, gs, st);
   if (M == 2) return launch_rows<8, 2>(x, w, s, y, M, N, K, gs, st);

@@ -62,7 +62,8 @@ def test_workspace_too_small_is_rejected(sq8):
 def test_path_selection(sq8):
     assert sq8.path_name(1, 4096, 4096, 64) == "gemv"
     assert sq8.path_name(2, 4096, 4096, 64) == "gemv"
-    assert sq8.path_name(3, 4096, 4096, 64) == "mfma"
+    assert sq8.path_name(4, 4096, 4096, 64) == "gemv"      # 4 token rows still fit the LDS stage
+    assert sq8.path_name(3, 4096, 14336, 64) == "mfma"
     assert sq8.path_name(2048, 4096, 4096, 64) == "mfma"
     assert sq8.path_name(8, 4096, 4096, 32) == "gemv"      # MFMA steps are whole 64-wide groups
     assert sq8.path_name(1, 4096, 100, 4) == "generic"   # gs not a multiple of 16

@@ -52,7 +52,7 @@ def test_small_shapes(sq8, dev, M, N, K):
     check(run(sq8, dev, x, q, s, 64), o.matmul_f64(x, q, s, 64), f"M={M} N={N} K={K}")
 
 
-@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("M", [1, 2, 4])
 @pytest.mark.parametrize("N,K,gs", [(33, 8192, 64), (50, 9280, 64), (17, 14336, 64),
                                     (9, 14336, 32), (21, 16000, 64), (300, 7168, 64)])
 def test_long_rows_decode(sq8, dev, M, N, K, gs):
