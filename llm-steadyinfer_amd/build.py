@@ -18,8 +18,7 @@ OBJ_DIR = PKG_DIR / "_build"
 LIB_PATH = PKG_DIR / "libsq8.so"
 CPP_DIR = PKG_DIR / "cpp"
 OP_LIB_PATH = PKG_DIR / "libsq8_op.so"
-CPP_TEST_SRC = REPO_DIR / "tests" / "cpp" / "test_matmul_layer.cpp"
-CPP_TEST_BIN = OBJ_DIR / "test_matmul_layer"
+CPP_TEST_NAMES = ("test_matmul_layer", "test_model_file")
 ORACLE_LIB = REPO_DIR / "oracle" / "_ref" / "libsq8_oracle.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -67,18 +66,22 @@ def build_op_layer(verbose: bool = False) -> Path:
     return OP_LIB_PATH
 
 
-def build_cpp_tests(verbose: bool = False) -> Path:
-    """Compile the C++ op-layer test program (links libsq8_op.so, libsq8.so and the oracle)."""
+def build_cpp_tests(verbose: bool = False) -> list:
+    """Compile the C++ test programs (link libsq8_op.so, libsq8.so and the oracle as checker)."""
     if not ORACLE_LIB.exists():
         raise RuntimeError(f"oracle library missing: {ORACLE_LIB}")
-    inc = ["-I", str(CPP_DIR / "include")]
-    obj = _compile(CPP_TEST_SRC, inc)
-    _link([obj], CPP_TEST_BIN, ["-L", str(PKG_DIR), "-lsq8_op", "-lsq8", "-L",
-                                 str(ORACLE_LIB.parent), "-lsq8_oracle",
-                                 "-Wl,-rpath,$ORIGIN/..", "-Wl,-rpath,$ORIGIN/../../oracle/_ref"])
-    if verbose:
-        print(f"built {CPP_TEST_BIN}")
-    return CPP_TEST_BIN
+    inc = ["-I", str(CPP_DIR / "include"), "-I", str(REPO_DIR / "tests" / "cpp")]
+    out = []
+    for name in CPP_TEST_NAMES:
+        obj = _compile(REPO_DIR / "tests" / "cpp" / f"{name}.cpp", inc)
+        binary = OBJ_DIR / name
+        _link([obj], binary, ["-L", str(PKG_DIR), "-lsq8_op", "-lsq8", "-L",
+                              str(ORACLE_LIB.parent), "-lsq8_oracle",
+                              "-Wl,-rpath,$ORIGIN/..", "-Wl,-rpath,$ORIGIN/../../oracle/_ref"])
+        if verbose:
+            print(f"built {binary}")
+        out.append(binary)
+    return out
 
 
 def build(verbose: bool = False) -> Path:

@@ -15,6 +15,7 @@
 #include <vector>
 #include "kernels/kernels_interface.h"
 #include "op/matmul.h"
+#include "test_util.h"
 
 extern "C" {
 void sq8o_quantize(const float* w, int64_t numel, int gs, int8_t* q, float* s);
@@ -24,27 +25,8 @@ void sq8o_matmul_f64(const float* x, const int8_t* w, const float* s, double* y,
 
 namespace {
 
-int g_failures = 0;
-#define EXPECT(cond, msg)                                            \
-  do {                                                               \
-    if (!(cond)) {                                                   \
-      std::printf("FAIL %s:%d %s (%s)\n", __FILE__, __LINE__, #cond, msg); \
-      ++g_failures;                                                  \
-    }                                                                \
-  } while (0)
-
-// Deterministic N(0, sigma) values (Box-Muller over a 64-bit LCG).
-struct Rng {
-  uint64_t s;
-  explicit Rng(uint64_t seed) : s(seed * 6364136223846793005ull + 1442695040888963407ull) {}
-  double uni() {
-    s = s * 6364136223846793005ull + 1442695040888963407ull;
-    return ((s >> 11) + 0.5) / 9007199254740992.0;
-  }
-  float normal(float sigma) {
-    return static_cast<float>(sigma * std::sqrt(-2.0 * std::log(uni())) * std::cos(6.283185307179586 * uni()));
-  }
-};
+using sq8test::Rng;
+using sq8test::max_rel_err;
 
 // Weight block as the model file stores it: int8 [N][K] then fp32 [N*K/gs] scales.
 std::vector<uint8_t> make_weight_block(int N, int K, int gs, uint64_t seed) {
@@ -109,18 +91,6 @@ void test_host() {
   std::printf("host checks done\n");
 }
 
-double max_rel_err(const std::vector<float>& y, const std::vector<double>& r, double* norm) {
-  double amax = 0, dmax = 0, elem = 0;
-  for (double v : r) amax = std::fmax(amax, std::fabs(v));
-  for (size_t i = 0; i < y.size(); ++i) {
-    const double d = std::fabs(y[i] - r[i]);
-    dmax = std::fmax(dmax, d);
-    elem = std::fmax(elem, d / std::fmax(std::fabs(r[i]), 1e-3 * amax));
-  }
-  *norm = amax > 0 ? dmax / amax : dmax;
-  return elem;
-}
-
 void run_case(int M, int N, int K, int gs, bool one_d, bool with_bias) {
   auto blob = make_weight_block(N, K, gs, 100 + M + N);
   Rng r(7 + M);
@@ -164,7 +134,7 @@ void run_case(int M, int N, int K, int gs, bool one_d, bool with_bias) {
   std::printf("%s M=%d N=%d K=%d gs=%d %s%s elem=%.2e norm=%.2e\n", ok ? "PASS" : "FAIL", M, N, K, gs,
               one_d ? "1-D" : "2-D", with_bias ? " +bias" : "", elem, norm);
   std::fflush(stdout);
-  if (!ok) ++g_failures;
+  if (!ok) ++sq8test::failures();
 }
 
 void test_gpu() {
@@ -193,6 +163,6 @@ int main(int argc, char** argv) {
     std::printf("usage: %s host|gpu\n", argv[0]);
     return 2;
   }
-  std::printf("%s: %d failure(s)\n", mode.c_str(), g_failures);
-  return g_failures == 0 ? 0 : 1;
+  std::printf("%s: %d failure(s)\n", mode.c_str(), sq8test::failures());
+  return sq8test::failures() == 0 ? 0 : 1;
 }
