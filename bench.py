@@ -44,7 +44,9 @@ METRIC = "INT8 GEMV HBM GB/s (% of peak) + decode tokens/s, Llama-3-8B shapes, 1
 
 def load_pkg():
     name = "llm_steadyinfer_amd"
-    spec = importlib.util.spec_from_file_location(name, REPO / "llm-steadyinfer_amd" / "__init__.py")
+    pkg_dir = REPO / "llm-steadyinfer_amd"
+    spec = importlib.util.spec_from_file_location(name, pkg_dir / "__init__.py",
+                                                  submodule_search_locations=[str(pkg_dir)])
     mod = importlib.util.module_from_spec(spec)
     sys.modules[name] = mod
     spec.loader.exec_module(mod)

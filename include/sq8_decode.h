@@ -1,0 +1,89 @@
+/*
+ * sq8_decode.h - C ABI of the single-sequence decode operators around the INT8 matmul on gfx950.
+ *
+ * These are the layers a decoder step runs between the quantised projections (reference:
+ * LLamaModel / Qwen2Model single-token forward, src/source/model/qwen2.cpp:690-830 and
+ * src/source/model/llama3.cpp:705-818). Each entry point replaces one reference kernel launcher,
+ * cited at its declaration. Conventions are those of sq8.h: device pointers owned by the caller,
+ * asynchronous on `hip_stream`, nothing allocated, negative status codes on error.
+ *
+ * Positions and tokens are read from (and written to) device memory, so a whole decode step can
+ * be captured once into a HIP graph and replayed for every token.
+ *
+ * KV cache layout (one buffer per layer for keys, one for values): [max_seq][kv_dim] fp32, the
+ * reference's single-sequence layout (mha_kernel.cu:58, "[num_layers, seq, kv_dim]").
+ */
+#ifndef SQ8_DECODE_H_
+#define SQ8_DECODE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* out[i][:] = table[tokens[i]][:] for i < n; a token outside [0, vocab) leaves its row untouched
+ * (emb_kernel_cu_fp32, src/source/op/kernels/cuda/emb_kernel.cu:3-21). */
+int sq8_embedding(const float* table, int vocab, int dim, const int32_t* tokens, int n, float* out,
+                  void* hip_stream);
+
+/* out[r][:] = rsqrt(mean(x[r][:]^2) + eps) * x[r][:] * w[:] for each of `rows` rows
+ * (row_rmsnorm_f32 / row_rmsnorm_f32_dim, src/source/op/kernels/cuda/rmsnorm_kernel.cu:8-160;
+ * the reference uses eps = 1e-6). */
+int sq8_rmsnorm(const float* x, const float* w, float* out, int rows, int dim, float eps,
+                void* hip_stream);
+
+/* Residual add then RMSNorm in one pass: x[r][:] += res[r][:] (written back), then
+ * out[r][:] = rmsnorm(x[r][:]) * w. Fuses the reference's VecAddLayer and RmsNormLayer
+ * (qwen2.cpp:780-790; add_kernel.cu, rmsnorm_kernel.cu). */
+int sq8_add_rmsnorm(float* x, const float* res, const float* w, float* out, int rows, int dim,
+                    float eps, void* hip_stream);
+
+/* RoPE tables: sin/cos[pos][j] = sin/cos(pos / theta^(j / head_size)) for pos < max_seq,
+ * j < head_size (sin_cos_calc, src/source/op/kernels/cuda/rope_kernel.cu:39-52). */
+int sq8_rope_tables(float* sin_cache, float* cos_cache, int head_size, int max_seq, float theta,
+                    void* hip_stream);
+
+/* On the fused projection output qkv = [q (dim) | k (kv_dim) | v (kv_dim)] of one token at
+ * position *pos: rotates q in place and writes the rotated k and the unchanged v into row *pos of
+ * the layer's key and value caches. Pairs (i, i + head_size/2) of each head rotate by the angle
+ * at table column 2i (rope_kernel_cu_fp32, rope_kernel.cu:4-37). */
+int sq8_rope_kv(float* qkv, int dim, int kv_dim, int head_size, const int32_t* pos,
+                const float* sin_cache, const float* cos_cache, float* key_cache,
+                float* value_cache, int max_seq, void* hip_stream);
+
+/* Causal attention of one query token at position *pos over cache rows 0..*pos:
+ * out[h] = softmax_t(q[h] . K[t][g(h)] / sqrt(head_size)) . V[t][g(h)] with the grouped-query
+ * head map g(h) = h * kv_head_num / head_num (flash_decoding_kernel + combine,
+ * src/source/op/kernels/cuda/mha_kernel.cu:178-341). */
+int sq8_attention_decode(const float* q, const float* key_cache, const float* value_cache,
+                         const int32_t* pos, float* out, int head_num, int kv_head_num,
+                         int head_size, int max_seq, void* hip_stream);
+
+/* out[i] = silu(a[i]) * b[i], silu(v) = v / (1 + exp(-v)) (swiglu_kernel_cu_fp32,
+ * src/source/op/kernels/cuda/swiglu_kernel.cu:4-21). `out` may alias `a`. */
+int sq8_swiglu(const float* a, const float* b, float* out, int n, void* hip_stream);
+
+/* x[i] += y[i] (add_kernel.cu, used in place as the residual add). */
+int sq8_add(float* x, const float* y, int n, void* hip_stream);
+
+/* *out = index of the first maximum of logits[0..n) (ArgmaxSampler::sample,
+ * src/source/sampler/argmax_sampler.cpp:5-13: std::max_element). */
+int sq8_argmax(const float* logits, int n, int32_t* out, void* hip_stream);
+
+/* Group absmax quantiser on the device, bit-identical to the benchmark quantiser the model files
+ * use: per flat group of group_size values s = absmax / 127, q = round-half-away(w / s) clamped
+ * to +-127, an all-zero group gives s = 0 and q = 0. numel % group_size must be 0. */
+int sq8_quantize(const float* w, int64_t numel, int group_size, int8_t* q, float* scales,
+                 void* hip_stream);
+
+/* Decode-loop bookkeeping on the device: *pos += 1 and *token = *next (so a captured step feeds
+ * its own output back). No reference counterpart (the reference updates these on the host). */
+int sq8_step_advance(int32_t* pos, int32_t* token, const int32_t* next, void* hip_stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SQ8_DECODE_H_ */

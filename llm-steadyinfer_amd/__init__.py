@@ -22,6 +22,10 @@ SQ8_ERR_LAUNCH = -5
 SQ8_ERR_DEVICE = -6
 
 EXPORTED_SYMBOLS = ("sq8_matmul", "sq8_workspace_bytes", "sq8_status_string", "sq8_path_name")
+# include/sq8_decode.h
+DECODE_SYMBOLS = ("sq8_embedding", "sq8_rmsnorm", "sq8_add_rmsnorm", "sq8_rope_tables", "sq8_rope_kv",
+                  "sq8_attention_decode", "sq8_swiglu", "sq8_add", "sq8_argmax", "sq8_quantize",
+                  "sq8_step_advance")
 
 _lib = None
 
@@ -49,6 +53,24 @@ def lib() -> ctypes.CDLL:
         L.sq8_status_string.restype = ctypes.c_char_p
         L.sq8_path_name.argtypes = [I, I, I, I]
         L.sq8_path_name.restype = ctypes.c_char_p
+        f32 = ctypes.c_float
+        sigs = {
+            "sq8_embedding": [vp, I, I, vp, I, vp, vp],
+            "sq8_rmsnorm": [vp, vp, vp, I, I, f32, vp],
+            "sq8_add_rmsnorm": [vp, vp, vp, vp, I, I, f32, vp],
+            "sq8_rope_tables": [vp, vp, I, I, f32, vp],
+            "sq8_rope_kv": [vp, I, I, I, vp, vp, vp, vp, vp, I, vp],
+            "sq8_attention_decode": [vp, vp, vp, vp, vp, I, I, I, I, vp],
+            "sq8_swiglu": [vp, vp, vp, I, vp],
+            "sq8_add": [vp, vp, I, vp],
+            "sq8_argmax": [vp, I, vp, vp],
+            "sq8_quantize": [vp, ctypes.c_int64, I, vp, vp, vp],
+            "sq8_step_advance": [vp, vp, vp, vp],
+        }
+        for name, args in sigs.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = I
         _lib = L
     return _lib
 
@@ -116,3 +138,77 @@ def matmul(x, w, scales, y=None, group_size: int = 64, workspace: Workspace | No
     if rc != SQ8_OK:
         raise Sq8Error(rc)
     return y.reshape(-1) if squeeze else y
+
+
+# ----------------------------------------------------------------------------- decode operators
+# Thin wrappers over include/sq8_decode.h taking torch device tensors; each raises Sq8Error on a
+# non-zero status. `stream` defaults to torch's current stream.
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _call(name: str, *args, stream=None):
+    import torch
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    rc = int(getattr(lib(), name)(*args, stream.cuda_stream))
+    if rc != SQ8_OK:
+        raise Sq8Error(rc)
+
+
+def embedding(table, tokens, out, stream=None):
+    """out[i] = table[tokens[i]] (tokens int32 on the device)."""
+    vocab, dim = table.shape
+    _call("sq8_embedding", _ptr(table), vocab, dim, _ptr(tokens), tokens.numel(), _ptr(out),
+          stream=stream)
+
+
+def rmsnorm(x, w, out, eps: float = 1e-6, stream=None):
+    dim = w.numel()
+    _call("sq8_rmsnorm", _ptr(x), _ptr(w), _ptr(out), x.numel() // dim, dim, eps, stream=stream)
+
+
+def add_rmsnorm(x, res, w, out, eps: float = 1e-6, stream=None):
+    """x += res (in place), out = rmsnorm(x) * w."""
+    dim = w.numel()
+    _call("sq8_add_rmsnorm", _ptr(x), _ptr(res), _ptr(w), _ptr(out), x.numel() // dim, dim, eps,
+          stream=stream)
+
+
+def rope_tables(sin_cache, cos_cache, head_size: int, max_seq: int, theta: float, stream=None):
+    _call("sq8_rope_tables", _ptr(sin_cache), _ptr(cos_cache), head_size, max_seq, theta,
+          stream=stream)
+
+
+def rope_kv(qkv, dim: int, kv_dim: int, head_size: int, pos, sin_cache, cos_cache, kcache, vcache,
+            max_seq: int, stream=None):
+    _call("sq8_rope_kv", _ptr(qkv), dim, kv_dim, head_size, _ptr(pos), _ptr(sin_cache),
+          _ptr(cos_cache), _ptr(kcache), _ptr(vcache), max_seq, stream=stream)
+
+
+def attention_decode(q, kcache, vcache, pos, out, head_num: int, kv_head_num: int, head_size: int,
+                     max_seq: int, stream=None):
+    _call("sq8_attention_decode", _ptr(q), _ptr(kcache), _ptr(vcache), _ptr(pos), _ptr(out),
+          head_num, kv_head_num, head_size, max_seq, stream=stream)
+
+
+def swiglu(a, b, out, stream=None):
+    _call("sq8_swiglu", _ptr(a), _ptr(b), _ptr(out), a.numel(), stream=stream)
+
+
+def add(x, y, stream=None):
+    _call("sq8_add", _ptr(x), _ptr(y), x.numel(), stream=stream)
+
+
+def argmax(logits, out, stream=None):
+    _call("sq8_argmax", _ptr(logits), logits.numel(), _ptr(out), stream=stream)
+
+
+def quantize(w, q, scales, group_size: int = 64, stream=None):
+    _call("sq8_quantize", _ptr(w), w.numel(), group_size, _ptr(q), _ptr(scales), stream=stream)
+
+
+def step_advance(pos, token, next_token, stream=None):
+    _call("sq8_step_advance", _ptr(pos), _ptr(token), _ptr(next_token), stream=stream)

@@ -9,21 +9,25 @@ import pytest
 from conftest import REPO
 
 HEADER = REPO / "include" / "sq8.h"
+HEADERS = sorted((REPO / "include").glob("*.h"))
 
 
-def declared_functions():
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(sq8_[a-z0-9_]+)\s*\(", text)))
+def declared_functions(headers=(HEADER,)):
+    names = set()
+    for h in headers:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(sq8_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declares_expected(sq8):
     assert declared_functions() == sorted(sq8.EXPORTED_SYMBOLS)
+    assert declared_functions(HEADERS) == sorted(sq8.EXPORTED_SYMBOLS + sq8.DECODE_SYMBOLS)
 
 
 def test_library_exports_every_declared_symbol(sq8):
     lib = sq8.lib()
-    for name in declared_functions():
+    for name in declared_functions(HEADERS):
         assert hasattr(lib, name), name
 
 

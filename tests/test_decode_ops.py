@@ -1,0 +1,177 @@
+"""The decode operators of include/sq8_decode.h against the numpy restatement of the reference
+kernels (oracle/decode_oracle.py). CPU tests cover argument validation only (no device work)."""
+import numpy as np
+import pytest
+
+from oracle import decode_oracle as do
+from oracle import sq8_oracle as o
+
+FAKE = 0x1000  # never dereferenced: validation fails first
+
+
+def test_decode_ops_reject_bad_arguments(sq8):
+    L = sq8.lib()
+    assert L.sq8_rmsnorm(None, FAKE, FAKE, 1, 8, 1e-6, None) == sq8.SQ8_ERR_NULL
+    assert L.sq8_rmsnorm(FAKE, FAKE, FAKE, 0, 8, 1e-6, None) == sq8.SQ8_ERR_DIMS
+    assert L.sq8_add_rmsnorm(FAKE, None, FAKE, FAKE, 1, 8, 1e-6, None) == sq8.SQ8_ERR_NULL
+    assert L.sq8_rope_kv(FAKE, 96, 64, 64, FAKE, FAKE, FAKE, FAKE, FAKE, 16, None) == sq8.SQ8_ERR_DIMS
+    assert L.sq8_rope_kv(FAKE, 128, 256, 64, FAKE, FAKE, FAKE, FAKE, FAKE, 16, None) == sq8.SQ8_ERR_DIMS
+    assert L.sq8_attention_decode(FAKE, FAKE, FAKE, FAKE, FAKE, 6, 4, 64, 16, None) == sq8.SQ8_ERR_DIMS
+    assert L.sq8_attention_decode(FAKE, FAKE, FAKE, FAKE, FAKE, 8, 2, 512, 16, None) == sq8.SQ8_ERR_DIMS
+    assert L.sq8_attention_decode(FAKE, FAKE, FAKE, FAKE, FAKE, 8, 2, 64, 1 << 20, None) == sq8.SQ8_ERR_DIMS
+    assert L.sq8_quantize(FAKE, 100, 64, FAKE, FAKE, None) == sq8.SQ8_ERR_GROUP
+    assert L.sq8_argmax(FAKE, 0, FAKE, None) == sq8.SQ8_ERR_DIMS
+    assert L.sq8_swiglu(FAKE, None, FAKE, 4, None) == sq8.SQ8_ERR_NULL
+    assert L.sq8_embedding(FAKE, 0, 8, FAKE, 1, FAKE, None) == sq8.SQ8_ERR_DIMS
+    assert L.sq8_step_advance(FAKE, None, FAKE, None) == sq8.SQ8_ERR_NULL
+
+
+def _t(a, dev, dtype=None):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t if dtype is None else t.to(dtype)
+
+
+def _close(got, ref, rtol, label):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    err = np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30)
+    print(f"{label}: max err / max |ref| = {err:.2e}")
+    assert np.all(np.isfinite(got)) and err <= rtol, (label, err)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,dim", [(1, 1536), (3, 4096), (2, 100)])
+def test_rmsnorm_and_add_rmsnorm(sq8, dev, rows, dim):
+    import torch
+    rng = np.random.default_rng(rows + dim)
+    x = rng.standard_normal((rows, dim)).astype(np.float32) * 3
+    r = rng.standard_normal((rows, dim)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, dim).astype(np.float32)
+    out = torch.empty((rows, dim), device=dev)
+    sq8.rmsnorm(_t(x, dev), _t(w, dev), out)
+    _close(out.cpu().numpy(), do.rmsnorm(x, w), 2e-6, "rmsnorm")
+    xt = _t(x, dev)
+    sq8.add_rmsnorm(xt, _t(r, dev), _t(w, dev), out)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(xt.cpu().numpy(), x + r)
+    _close(out.cpu().numpy(), do.rmsnorm(x + r, w), 2e-6, "add_rmsnorm")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("head_size,theta", [(64, 1e6), (128, 5e5)])
+def test_rope_tables(sq8, dev, head_size, theta):
+    import torch
+    max_seq = 512
+    sin = torch.empty((max_seq, head_size), device=dev)
+    cos = torch.empty((max_seq, head_size), device=dev)
+    sq8.rope_tables(sin, cos, head_size, max_seq, theta)
+    s_ref, c_ref = do.rope_tables(head_size, max_seq, theta)
+    # The angle is formed in fp32 (pos * freq), as the reference does: allow its rounding.
+    tol = 1e-6 + 2e-7 * np.arange(max_seq)[:, None]
+    assert np.all(np.abs(sin.cpu().numpy() - s_ref) <= tol)
+    assert np.all(np.abs(cos.cpu().numpy() - c_ref) <= tol)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads,kv_heads,hs,pos", [(12, 2, 128, 0), (12, 2, 128, 37), (4, 4, 64, 200)])
+def test_rope_kv_writes_cache(sq8, dev, heads, kv_heads, hs, pos):
+    import torch
+    dim, kv = heads * hs, kv_heads * hs
+    max_seq = 256
+    rng = np.random.default_rng(pos + hs)
+    qkv = rng.standard_normal(dim + 2 * kv).astype(np.float32)
+    sin = torch.empty((max_seq, hs), device=dev)
+    cos = torch.empty((max_seq, hs), device=dev)
+    sq8.rope_tables(sin, cos, hs, max_seq, 1e6)
+    kc = torch.full((max_seq, kv), -7.0, device=dev)
+    vc = torch.full((max_seq, kv), -7.0, device=dev)
+    qt = _t(qkv, dev)
+    sq8.rope_kv(qt, dim, kv, hs, _t(np.array([pos], np.int32), dev), sin, cos, kc, vc, max_seq)
+    torch.cuda.synchronize()
+    s_np, c_np = sin.cpu().numpy().astype(np.float64), cos.cpu().numpy().astype(np.float64)
+    _close(qt[:dim].cpu().numpy(), do.rope(qkv[:dim], heads, hs, pos, s_np, c_np), 1e-6, "q")
+    _close(kc[pos].cpu().numpy(), do.rope(qkv[dim:dim + kv], kv_heads, hs, pos, s_np, c_np), 1e-6, "k")
+    np.testing.assert_array_equal(vc[pos].cpu().numpy(), qkv[dim + kv:])
+    other = np.delete(np.arange(max_seq), pos)
+    assert np.all(kc.cpu().numpy()[other] == -7.0) and np.all(vc.cpu().numpy()[other] == -7.0)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads,kv_heads,hs,pos", [(12, 2, 128, 0), (12, 2, 128, 191), (32, 8, 128, 700),
+                                                   (4, 1, 64, 5)])
+def test_attention_decode(sq8, dev, heads, kv_heads, hs, pos):
+    import torch
+    max_seq = 1024
+    kv = kv_heads * hs
+    rng = np.random.default_rng(pos * 3 + heads)
+    q = rng.standard_normal(heads * hs).astype(np.float32)
+    kc = rng.standard_normal((max_seq, kv)).astype(np.float32)
+    vc = rng.standard_normal((max_seq, kv)).astype(np.float32)
+    out = torch.empty(heads * hs, device=dev)
+    sq8.attention_decode(_t(q, dev), _t(kc, dev), _t(vc, dev), _t(np.array([pos], np.int32), dev),
+                         out, heads, kv_heads, hs, max_seq)
+    _close(out.cpu().numpy(), do.attention(q, kc, vc, pos, heads, kv_heads, hs), 2e-6, "attention")
+
+
+@pytest.mark.gpu
+def test_swiglu_add_embedding(sq8, dev):
+    import torch
+    rng = np.random.default_rng(0)
+    a = (rng.standard_normal(8960) * 4).astype(np.float32)
+    b = rng.standard_normal(8960).astype(np.float32)
+    out = torch.empty(8960, device=dev)
+    sq8.swiglu(_t(a, dev), _t(b, dev), out)
+    _close(out.cpu().numpy(), do.swiglu(a, b), 1e-6, "swiglu")
+    x = _t(a, dev)
+    sq8.add(x, _t(b, dev))
+    np.testing.assert_array_equal(x.cpu().numpy(), a + b)
+    table = rng.standard_normal((300, 96)).astype(np.float32)
+    toks = np.array([5, 299, 0, 300, -1], np.int32)   # the last two are out of range
+    emb = torch.full((5, 96), 3.0, device=dev)
+    sq8.embedding(_t(table, dev), _t(toks, dev), emb)
+    e = emb.cpu().numpy()
+    np.testing.assert_array_equal(e[:3], table[[5, 299, 0]])
+    assert np.all(e[3:] == 3.0)
+
+
+@pytest.mark.gpu
+def test_argmax_first_maximum(sq8, dev):
+    import torch
+    rng = np.random.default_rng(1)
+    out = torch.empty(1, dtype=torch.int32, device=dev)
+    for n in (1, 7, 1000, 151936):
+        v = rng.standard_normal(n).astype(np.float32)
+        sq8.argmax(_t(v, dev), out)
+        assert int(out.item()) == do.argmax_first(v), n
+    v = rng.standard_normal(151936).astype(np.float32)
+    v[[90000, 1234, 151935]] = 50.0            # ties: the first index wins
+    sq8.argmax(_t(v, dev), out)
+    assert int(out.item()) == 1234
+    v = np.full(5000, -np.inf, np.float32)
+    sq8.argmax(_t(v, dev), out)
+    assert int(out.item()) == 0
+
+
+@pytest.mark.gpu
+def test_device_quantiser_matches_oracle(sq8, dev):
+    import torch
+    rng = np.random.default_rng(2)
+    w = (rng.standard_normal(64 * 4096) * 10.0 ** rng.uniform(-5, 5, 64 * 4096)).astype(np.float32)
+    w[:64] = 0
+    w[64:128] = np.float32(127.5) * np.arange(64, dtype=np.float32) / 63
+    q = torch.empty(w.size, dtype=torch.int8, device=dev)
+    s = torch.empty(w.size // 64, device=dev)
+    sq8.quantize(_t(w, dev), q, s, 64)
+    q2, s2 = o.quantize(w, 64)
+    np.testing.assert_array_equal(q.cpu().numpy(), q2.reshape(-1))
+    np.testing.assert_array_equal(s.cpu().numpy(), s2)
+
+
+@pytest.mark.gpu
+def test_step_advance(sq8, dev):
+    import torch
+    pos = torch.tensor([41], dtype=torch.int32, device=dev)
+    tok = torch.tensor([3], dtype=torch.int32, device=dev)
+    nxt = torch.tensor([977], dtype=torch.int32, device=dev)
+    sq8.step_advance(pos, tok, nxt)
+    assert int(pos.item()) == 42 and int(tok.item()) == 977
