@@ -69,8 +69,13 @@ int sq8_swiglu(const float* a, const float* b, float* out, int n, void* hip_stre
 int sq8_add(float* x, const float* y, int n, void* hip_stream);
 
 /* *out = index of the first maximum of logits[0..n) (ArgmaxSampler::sample,
- * src/source/sampler/argmax_sampler.cpp:5-13: std::max_element). */
-int sq8_argmax(const float* logits, int n, int32_t* out, void* hip_stream);
+ * src/source/sampler/argmax_sampler.cpp:5-13: std::max_element). One launch over many
+ * workgroups: the workspace (sq8_argmax_workspace_bytes(n)) holds their winners and a ticket; it
+ * must be zero before its first use and is left with the ticket zero. Calls that overlap in time
+ * on one workspace race. NaN never wins; all-NaN input gives 0. */
+size_t sq8_argmax_workspace_bytes(int n);
+int sq8_argmax(const float* logits, int n, int32_t* out, void* workspace, size_t workspace_bytes,
+               void* hip_stream);
 
 /* Group absmax quantiser on the device, bit-identical to the benchmark quantiser the model files
  * use: per flat group of group_size values s = absmax / 127, q = round-half-away(w / s) clamped

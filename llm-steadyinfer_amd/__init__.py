@@ -24,8 +24,8 @@ SQ8_ERR_DEVICE = -6
 EXPORTED_SYMBOLS = ("sq8_matmul", "sq8_workspace_bytes", "sq8_status_string", "sq8_path_name")
 # include/sq8_decode.h
 DECODE_SYMBOLS = ("sq8_embedding", "sq8_rmsnorm", "sq8_add_rmsnorm", "sq8_rope_tables", "sq8_rope_kv",
-                  "sq8_attention_decode", "sq8_swiglu", "sq8_add", "sq8_argmax", "sq8_quantize",
-                  "sq8_step_advance")
+                  "sq8_attention_decode", "sq8_swiglu", "sq8_add", "sq8_argmax_workspace_bytes",
+                  "sq8_argmax", "sq8_quantize", "sq8_step_advance")
 
 _lib = None
 
@@ -63,7 +63,7 @@ def lib() -> ctypes.CDLL:
             "sq8_attention_decode": [vp, vp, vp, vp, vp, I, I, I, I, vp],
             "sq8_swiglu": [vp, vp, vp, I, vp],
             "sq8_add": [vp, vp, I, vp],
-            "sq8_argmax": [vp, I, vp, vp],
+            "sq8_argmax": [vp, I, vp, vp, sz, vp],
             "sq8_quantize": [vp, ctypes.c_int64, I, vp, vp, vp],
             "sq8_step_advance": [vp, vp, vp, vp],
         }
@@ -71,6 +71,8 @@ def lib() -> ctypes.CDLL:
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = I
+        L.sq8_argmax_workspace_bytes.argtypes = [I]
+        L.sq8_argmax_workspace_bytes.restype = sz
         _lib = L
     return _lib
 
@@ -202,8 +204,13 @@ def add(x, y, stream=None):
     _call("sq8_add", _ptr(x), _ptr(y), x.numel(), stream=stream)
 
 
-def argmax(logits, out, stream=None):
-    _call("sq8_argmax", _ptr(logits), logits.numel(), _ptr(out), stream=stream)
+def argmax(logits, out, workspace: Workspace | None = None, stream=None):
+    """out[0] = first argmax of logits (int32 on the device)."""
+    n = logits.numel()
+    if workspace is None:
+        workspace = _default_ws.setdefault(str(logits.device) + ":argmax", Workspace(logits.device))
+    ws_ptr, ws_n = workspace.get(int(lib().sq8_argmax_workspace_bytes(n)))
+    _call("sq8_argmax", _ptr(logits), n, _ptr(out), ws_ptr or None, ws_n, stream=stream)
 
 
 def quantize(w, q, scales, group_size: int = 64, stream=None):

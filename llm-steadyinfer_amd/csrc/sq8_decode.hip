@@ -5,6 +5,7 @@
 // attention, vectorised elementwise kernels. Reductions run in a fixed order (wave butterflies,
 // then waves in index order), so every result is deterministic.
 #include <float.h>
+#include <limits.h>
 #include <math.h>
 #include "sq8.h"
 #include "sq8_common.h"
@@ -132,9 +133,14 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, int dim, int kv_dim, int
   }
 }
 
-// One workgroup per query head. Scores: wave w takes positions w, w + 4, ...; its lanes split the
-// head dimension and a butterfly sums the dot product. Softmax over the scores in LDS, then
-// thread d accumulates sum_t p_t * V[t][d] (coalesced across d) and divides by the sum.
+// One workgroup per query head.
+//  * Scores: thread t owns cache position t (t, t + 256, ...) and reads its key row as float4
+//    loads that are all independent (one memory round trip per 256 positions); q is broadcast from
+//    LDS.
+//  * Softmax over the scores in LDS: workgroup max and sum (fixed order).
+//  * Values: wave w takes positions w, w + 4, ... and lane l the dims l, l + 64, ...; four
+//    positions per iteration keep four independent loads in flight; the four waves' partial sums
+//    meet in LDS in wave order.
 template <int HS_MAX>
 __global__ __launch_bounds__(kBlock) void attention_decode_kernel(
     const float* __restrict__ q, const float* __restrict__ kcache,
@@ -142,7 +148,9 @@ __global__ __launch_bounds__(kBlock) void attention_decode_kernel(
     float* __restrict__ out, int head_num, int kv_head_num, int head_size) {
   extern __shared__ float s_p[];  // [seq] scores, then probabilities
   __shared__ float red[kBlockWaves];
-  __shared__ float s_q[HS_MAX];
+  __shared__ __attribute__((aligned(16))) float s_q[HS_MAX];
+  __shared__ float s_part[kBlockWaves][HS_MAX];
+  constexpr int DPL = HS_MAX / kWave;  // head dims per lane in the value pass
   const int head = blockIdx.x;
   const int seq = *pos_ptr + 1;
   const int kv_dim = kv_head_num * head_size;
@@ -151,12 +159,32 @@ __global__ __launch_bounds__(kBlock) void attention_decode_kernel(
   for (int d = threadIdx.x; d < head_size; d += kBlock) s_q[d] = q[head * head_size + d];
   __syncthreads();
   const float scale = 1.f / sqrtf(static_cast<float>(head_size));
-  for (int t = wave; t < seq; t += kBlockWaves) {
+  const bool vec4 = (head_size % 4) == 0 && (kv_dim % 4) == 0 && (hoff % 4) == 0;
+  for (int t = threadIdx.x; t < seq; t += kBlock) {
     const float* krow = kcache + static_cast<size_t>(t) * kv_dim + hoff;
-    float dot = 0.f;
-    for (int d = lane; d < head_size; d += kWave) dot = fmaf(s_q[d], krow[d], dot);
-    dot = wave_sum(dot);
-    if (lane == 0) s_p[t] = dot * scale;
+    float a0 = 0.f, a1 = 0.f;
+    if (vec4) {
+#pragma unroll 4
+      for (int d = 0; d < head_size; d += 8) {
+        const float4 k0 = *reinterpret_cast<const float4*>(krow + d);
+        const float4 q0 = *reinterpret_cast<const float4*>(s_q + d);
+        a0 = fmaf(q0.x, k0.x, a0);
+        a0 = fmaf(q0.y, k0.y, a0);
+        a0 = fmaf(q0.z, k0.z, a0);
+        a0 = fmaf(q0.w, k0.w, a0);
+        if (d + 4 < head_size) {
+          const float4 k1 = *reinterpret_cast<const float4*>(krow + d + 4);
+          const float4 q1 = *reinterpret_cast<const float4*>(s_q + d + 4);
+          a1 = fmaf(q1.x, k1.x, a1);
+          a1 = fmaf(q1.y, k1.y, a1);
+          a1 = fmaf(q1.z, k1.z, a1);
+          a1 = fmaf(q1.w, k1.w, a1);
+        }
+      }
+    } else {
+      for (int d = 0; d < head_size; ++d) a0 = fmaf(s_q[d], krow[d], a0);
+    }
+    s_p[t] = (a0 + a1) * scale;
   }
   __syncthreads();
   float m = -FLT_MAX;
@@ -169,11 +197,42 @@ __global__ __launch_bounds__(kBlock) void attention_decode_kernel(
     l += p;
   }
   l = block_sum(l, red);  // its barriers also publish the probabilities
+  float acc[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+  const float* vbase = vcache + hoff + lane;
+  int t = wave;
+  for (; t + 3 * kBlockWaves < seq; t += 4 * kBlockWaves) {
+    float v[4][DPL];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int j = 0; j < DPL; ++j)
+        v[u][j] = lane + j * kWave < head_size
+                      ? vbase[static_cast<size_t>(t + u * kBlockWaves) * kv_dim + j * kWave]
+                      : 0.f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float p = s_p[t + u * kBlockWaves];
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) acc[j] = fmaf(p, v[u][j], acc[j]);
+    }
+  }
+  for (; t < seq; t += kBlockWaves) {
+    const float p = s_p[t];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j)
+      if (lane + j * kWave < head_size)
+        acc[j] = fmaf(p, vbase[static_cast<size_t>(t) * kv_dim + j * kWave], acc[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) s_part[wave][lane + j * kWave] = acc[j];
+  __syncthreads();
   for (int d = threadIdx.x; d < head_size; d += kBlock) {
-    const float* vcol = vcache + hoff + d;
-    float acc = 0.f;
-    for (int t = 0; t < seq; ++t) acc = fmaf(s_p[t], vcol[static_cast<size_t>(t) * kv_dim], acc);
-    out[head * head_size + d] = acc / l;
+    float o = s_part[0][d];
+#pragma unroll
+    for (int w = 1; w < kBlockWaves; ++w) o += s_part[w][d];
+    out[head * head_size + d] = o / l;
   }
 }
 
@@ -191,31 +250,57 @@ __global__ void add_kernel(float* __restrict__ x, const float* __restrict__ y, i
   if (i < n) x[i] += y[i];
 }
 
-// First maximum: each thread scans increasing indices keeping strict improvements, then the
-// workgroup reduces (value, index) pairs, preferring the larger value and, on ties, the smaller
-// index.
-constexpr int kArgmaxBlock = 1024;
-__global__ __launch_bounds__(kArgmaxBlock) void argmax_kernel(const float* __restrict__ logits,
-                                                              int n, int32_t* __restrict__ out) {
-  __shared__ float sv[kArgmaxBlock / kWave];
-  __shared__ int si[kArgmaxBlock / kWave];
+// First maximum over n values in one launch. Workgroup b scans the contiguous chunk
+// [b * kArgmaxChunk, ...) with independent float4 loads, reduces its (value, index) pairs in a
+// fixed order and publishes its winner with agent-scope relaxed stores; the last workgroup to take
+// the ticket compares the winners in chunk order and writes the index, then resets the ticket.
+// Order: the larger value wins; equal values keep the smaller index (std::max_element's first
+// maximum). NaN never wins; if nothing wins the result is 0.
+constexpr int kArgmaxChunk = kBlock * 16;
+
+__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+__global__ __launch_bounds__(kBlock) void argmax_kernel(const float* __restrict__ logits, int n,
+                                                        int32_t* __restrict__ out,
+                                                        float* __restrict__ wval,
+                                                        int* __restrict__ widx,
+                                                        unsigned* __restrict__ ticket) {
+  __shared__ float sv[kBlockWaves];
+  __shared__ int si[kBlockWaves];
+  __shared__ bool last;
+  const int base = blockIdx.x * kArgmaxChunk;
   float best = -INFINITY;
-  int bi = n;  // "none yet"
-  for (int i = threadIdx.x; i < n; i += kArgmaxBlock) {
-    const float v = logits[i];
-    if (v > best || (bi == n && v == best)) {
-      best = v;
-      bi = i;
+  int bi = INT_MAX;
+  const bool vec4 = (n % 4) == 0;
+  float v[16];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i0 = base + (threadIdx.x + j * kBlock) * 4;
+    if (vec4 && i0 + 3 < n) {
+      const float4 f = *reinterpret_cast<const float4*>(logits + i0);
+      v[4 * j] = f.x; v[4 * j + 1] = f.y; v[4 * j + 2] = f.z; v[4 * j + 3] = f.w;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[4 * j + c] = i0 + c < n ? logits[i0 + c] : -INFINITY;
     }
   }
-  auto better = [](float v, int i, float bv, int bidx) {
-    return v > bv || (v == bv && i < bidx);
-  };
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int i = base + (threadIdx.x + j * kBlock) * 4 + c;
+      if (i < n && (v[4 * j + c] > best || (bi == INT_MAX && v[4 * j + c] == best))) {
+        best = v[4 * j + c];
+        bi = i;
+      }
+    }
 #pragma unroll
   for (int off = 32; off >= 1; off /= 2) {
     const float ov = __shfl_xor(best, off, kWave);
     const int oi = __shfl_xor(bi, off, kWave);
-    if (better(ov, oi, best, bi)) {
+    if (argmax_better(ov, oi, best, bi)) {
       best = ov;
       bi = oi;
     }
@@ -227,14 +312,32 @@ __global__ __launch_bounds__(kArgmaxBlock) void argmax_kernel(const float* __res
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    float v = sv[0];
-    int idx = si[0];
-    for (int w = 1; w < kArgmaxBlock / kWave; ++w)
-      if (better(sv[w], si[w], v, idx)) {
-        v = sv[w];
-        idx = si[w];
+    float bv = sv[0];
+    int bidx = si[0];
+    for (int w = 1; w < kBlockWaves; ++w)
+      if (argmax_better(sv[w], si[w], bv, bidx)) {
+        bv = sv[w];
+        bidx = si[w];
       }
-    out[0] = idx < n ? idx : 0;
+    __hip_atomic_store(wval + blockIdx.x, bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(widx + blockIdx.x, bidx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           gridDim.x - 1;
+    if (last) {
+      float fv = -INFINITY;
+      int fi = INT_MAX;
+      for (unsigned b = 0; b < gridDim.x; ++b) {
+        const float cv = __hip_atomic_load(wval + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int ci = __hip_atomic_load(widx + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (argmax_better(cv, ci, fv, fi)) {
+          fv = cv;
+          fi = ci;
+        }
+      }
+      out[0] = fi < n ? fi : 0;
+      __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -358,11 +461,23 @@ int sq8_add(float* x, const float* y, int n, void* hip_stream) {
   return launched();
 }
 
-int sq8_argmax(const float* logits, int n, int32_t* out, void* hip_stream) {
+size_t sq8_argmax_workspace_bytes(int n) {
+  if (n <= 0) return 0;
+  const size_t blocks = (static_cast<size_t>(n) + kArgmaxChunk - 1) / kArgmaxChunk;
+  return 256 + blocks * (sizeof(float) + sizeof(int));
+}
+
+int sq8_argmax(const float* logits, int n, int32_t* out, void* workspace, size_t workspace_bytes,
+               void* hip_stream) {
   if (!logits || !out) return SQ8_ERR_NULL;
   if (n <= 0) return SQ8_ERR_DIMS;
-  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgmaxBlock), 0, stream_of(hip_stream), logits,
-                     n, out);
+  if (!workspace || workspace_bytes < sq8_argmax_workspace_bytes(n)) return SQ8_ERR_WORKSPACE;
+  const int blocks = (n + kArgmaxChunk - 1) / kArgmaxChunk;
+  unsigned* ticket = static_cast<unsigned*>(workspace);
+  float* wval = reinterpret_cast<float*>(static_cast<char*>(workspace) + 256);
+  int* widx = reinterpret_cast<int*>(wval + blocks);
+  hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(kBlock), 0, stream_of(hip_stream), logits,
+                     n, out, wval, widx, ticket);
   return launched();
 }
 

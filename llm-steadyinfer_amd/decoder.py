@@ -21,8 +21,8 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import (Workspace, add_rmsnorm, argmax, attention_decode, embedding, matmul, quantize,
-               rmsnorm, rope_kv, rope_tables, step_advance, swiglu)
+from . import (Workspace, add_rmsnorm, argmax, attention_decode, embedding, lib, matmul,
+               quantize, rmsnorm, rope_kv, rope_tables, step_advance, swiglu)
 from .model_file import ModelConfig, ModelFile
 
 EPS = 1e-6
@@ -57,6 +57,8 @@ class Int8Decoder:
         self.token = torch.zeros(1, **i32)
         self.next = torch.zeros(1, **i32)
         self.ws = Workspace(device)
+        self.argmax_ws = Workspace(device)  # sized now: nothing is allocated during capture
+        self.argmax_ws.get(int(lib().sq8_argmax_workspace_bytes(cfg.vocab)))
         self.graph = None
 
     # ------------------------------------------------------------------ construction
@@ -154,7 +156,7 @@ class Int8Decoder:
         if want_logits:
             add_rmsnorm(self.x, self.proj, w["norm"][2 * L], self.xn, EPS, stream=stream)
             self._mm(self.xn, w["cls"], self.logits, stream)
-            argmax(self.logits, self.next, stream=stream)
+            argmax(self.logits, self.next, workspace=self.argmax_ws, stream=stream)
             step_advance(self.pos, self.token, self.next, stream=stream)
         else:
             # A prompt token: the residual stream of the last layer is not needed further.

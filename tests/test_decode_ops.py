@@ -20,7 +20,9 @@ def test_decode_ops_reject_bad_arguments(sq8):
     assert L.sq8_attention_decode(FAKE, FAKE, FAKE, FAKE, FAKE, 8, 2, 512, 16, None) == sq8.SQ8_ERR_DIMS
     assert L.sq8_attention_decode(FAKE, FAKE, FAKE, FAKE, FAKE, 8, 2, 64, 1 << 20, None) == sq8.SQ8_ERR_DIMS
     assert L.sq8_quantize(FAKE, 100, 64, FAKE, FAKE, None) == sq8.SQ8_ERR_GROUP
-    assert L.sq8_argmax(FAKE, 0, FAKE, None) == sq8.SQ8_ERR_DIMS
+    assert L.sq8_argmax(FAKE, 0, FAKE, FAKE, 4096, None) == sq8.SQ8_ERR_DIMS
+    assert L.sq8_argmax(FAKE, 5000, FAKE, FAKE, 8, None) == sq8.SQ8_ERR_WORKSPACE
+    assert L.sq8_argmax_workspace_bytes(151936) == 256 + 38 * 8
     assert L.sq8_swiglu(FAKE, None, FAKE, 4, None) == sq8.SQ8_ERR_NULL
     assert L.sq8_embedding(FAKE, 0, 8, FAKE, 1, FAKE, None) == sq8.SQ8_ERR_DIMS
     assert L.sq8_step_advance(FAKE, None, FAKE, None) == sq8.SQ8_ERR_NULL
