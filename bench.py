@@ -16,7 +16,12 @@ The step's 129 launches are issued eagerly on one stream; `--graph` replays them
 instead (the reference captures its decode step in a CUDA graph, src/source/model/model.cpp:
 189-238). On MI355X the eager launches measured faster, so eager is the default.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu] [--graph]
+Decode tokens/s (the metric's second half) comes from config 4: a Qwen2-1.5B-shaped random-init
+INT8 model (28 layers, hidden 1536, 12 Q / 2 KV heads, FFN 8960, vocab 151936) decoding 128
+greedy tokens at batch 1 after a 64-token prompt, on the HIP decode stack (decoder.py), each token
+one HIP-graph replay; `--no-decode` skips it.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu] [--no-decode] [--graph]
        python bench.py --profile   # short run for rocprofv3 counter passes (see profiles/)
 """
 from __future__ import annotations
@@ -122,6 +127,46 @@ def cpu_baseline(torch, weights, budget_s=10.0):
                       f"{reps} reps in {el:.1f} s"}
 
 
+def decode_run(torch, n_prompt: int = 64, n_new: int = 128, seed: int = 0):
+    """Config 4: greedy decode on a Qwen2-1.5B-shaped random-init INT8 model (on-device init of the
+    model-file distribution). The prompt runs eagerly one token per step (not timed as decode);
+    the n_new decode tokens are graph replays timed with HIP events on the current stream."""
+    import importlib
+    import numpy as np
+    mf = importlib.import_module("llm_steadyinfer_amd.model_file")
+    dec = importlib.import_module("llm_steadyinfer_amd.decoder")
+    cfg = mf.QWEN2_1_5B
+    D = dec.Int8Decoder.random(cfg, max_seq=n_prompt + n_new, seed=seed)
+    prompt = np.random.default_rng(seed).integers(0, cfg.vocab, n_prompt).tolist()
+    D.generate(prompt, 4)                      # captures the graph, warms every kernel
+    st = torch.cuda.current_stream()
+    D.reset()
+    t0 = time.perf_counter()
+    for t in prompt[:-1]:
+        D.token.fill_(int(t))
+        D._launch_step(st, want_logits=False)
+    D.token.fill_(int(prompt[-1]))
+    torch.cuda.synchronize()
+    prompt_ms = (time.perf_counter() - t0) * 1e3
+    toks = torch.empty(n_new, dtype=torch.int32, device=D.device)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for i in range(n_new):
+        D.graph.replay()
+        toks[i:i + 1].copy_(D.token)
+    b.record(st)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / n_new
+    wb = D.weight_bytes()
+    return {"workload": "config 4: Qwen2-1.5B-shaped random-init INT8 model (28 layers, hidden "
+                        "1536, 12/2 heads, FFN 8960, vocab 151936, group 64), batch 1, "
+                        f"{n_prompt}-token prompt, {n_new} greedy tokens",
+            "tokens_per_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4),
+            "prompt_ms_eager": round(prompt_ms, 1), "weight_bytes_per_token": wb,
+            "weight_GBps": round(wb / ms / 1e6, 1), "launch": "hip_graph per token",
+            "first_tokens": toks[:8].cpu().tolist()}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -129,6 +174,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--graph", action="store_true", help="replay the step as one HIP graph")
     ap.add_argument("--profile", action="store_true",
@@ -261,6 +307,11 @@ def main():
                 del x, y, cs
             print(f"# sweep M={M} done", file=sys.stderr, flush=True)
 
+    decode = None
+    if not args.no_decode:
+        decode = decode_run(torch)
+        print(f"# decode done: {decode['tokens_per_s']} tokens/s", file=sys.stderr, flush=True)
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(torch, weights, args.cpu_seconds)
@@ -277,6 +328,8 @@ def main():
         "launch": "hip_graph" if args.graph else "eager",
         "graph_GBps": round(step_bytes / dt_graph / 1e9, 1) if dt_graph else None,
         "decode_matmul_tokens_per_s": round(1.0 / dt, 1),
+        "decode_tokens_per_s": decode["tokens_per_s"] if decode else None,
+        "decode": decode,
         "step_algo_bytes": step_bytes,
         "roofline": roofline,
         "cpu_baseline": cpu,
