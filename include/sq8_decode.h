@@ -77,6 +77,22 @@ size_t sq8_argmax_workspace_bytes(int n);
 int sq8_argmax(const float* logits, int n, int32_t* out, void* workspace, size_t workspace_bytes,
                void* hip_stream);
 
+/* Fused decode projections: y[N] = matmul(x', w, scales) for one token row, where x' is formed
+ * while the GEMV stages its input (no extra launch, no round trip through memory):
+ *   sq8_matmul_rmsnorm: r = x + res (res may be NULL: r = x), x' = rmsnorm(r) * norm_w with the
+ *     reference's RMSNorm; r is also written to x_out (may be NULL), which must not alias x or res.
+ *     Replaces the reference's add + RMSNorm + projection sequence (qwen2.cpp:780-800).
+ *   sq8_matmul_swiglu: gate_up = [a (K) | b (K)], x' = silu(a) * b; replaces SwiGLU + w2
+ *     (qwen2.cpp:800-815).
+ * Accepted shapes are those of the single-row GEMV: group_size % 16 == 0, K % group_size == 0,
+ * 4*K bytes within the 64 KiB activation stage, 16-byte aligned vectors and weights; otherwise
+ * SQ8_ERR_DIMS / SQ8_ERR_GROUP. No workspace. */
+int sq8_matmul_rmsnorm(const float* x, const float* res, float* x_out, const float* norm_w,
+                       float eps, const int8_t* w, const float* scales, float* y, int N, int K,
+                       int group_size, void* hip_stream);
+int sq8_matmul_swiglu(const float* gate_up, const int8_t* w, const float* scales, float* y, int N,
+                      int K, int group_size, void* hip_stream);
+
 /* Group absmax quantiser on the device, bit-identical to the benchmark quantiser the model files
  * use: per flat group of group_size values s = absmax / 127, q = round-half-away(w / s) clamped
  * to +-127, an all-zero group gives s = 0 and q = 0. numel % group_size must be 0. */

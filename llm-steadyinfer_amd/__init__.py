@@ -25,7 +25,8 @@ EXPORTED_SYMBOLS = ("sq8_matmul", "sq8_workspace_bytes", "sq8_status_string", "s
 # include/sq8_decode.h
 DECODE_SYMBOLS = ("sq8_embedding", "sq8_rmsnorm", "sq8_add_rmsnorm", "sq8_rope_tables", "sq8_rope_kv",
                   "sq8_attention_decode", "sq8_swiglu", "sq8_add", "sq8_argmax_workspace_bytes",
-                  "sq8_argmax", "sq8_quantize", "sq8_step_advance")
+                  "sq8_argmax", "sq8_quantize", "sq8_step_advance", "sq8_matmul_rmsnorm",
+                  "sq8_matmul_swiglu")
 
 _lib = None
 
@@ -66,6 +67,8 @@ def lib() -> ctypes.CDLL:
             "sq8_argmax": [vp, I, vp, vp, sz, vp],
             "sq8_quantize": [vp, ctypes.c_int64, I, vp, vp, vp],
             "sq8_step_advance": [vp, vp, vp, vp],
+            "sq8_matmul_rmsnorm": [vp, vp, vp, vp, f32, vp, vp, vp, I, I, I, vp],
+            "sq8_matmul_swiglu": [vp, vp, vp, vp, I, I, I, vp],
         }
         for name, args in sigs.items():
             fn = getattr(L, name)
@@ -219,3 +222,19 @@ def quantize(w, q, scales, group_size: int = 64, stream=None):
 
 def step_advance(pos, token, next_token, stream=None):
     _call("sq8_step_advance", _ptr(pos), _ptr(token), _ptr(next_token), stream=stream)
+
+
+def matmul_rmsnorm(x, res, x_out, norm_w, w, scales, y, group_size: int = 64, eps: float = 1e-6,
+                   stream=None):
+    """y = matmul(rmsnorm(x + res) * norm_w, w); x + res also written to x_out (res, x_out may be
+    None)."""
+    N, K = w.shape
+    _call("sq8_matmul_rmsnorm", _ptr(x), _ptr(res), _ptr(x_out), _ptr(norm_w), eps, _ptr(w),
+          _ptr(scales), _ptr(y), N, K, group_size, stream=stream)
+
+
+def matmul_swiglu(gate_up, w, scales, y, group_size: int = 64, stream=None):
+    """y = matmul(silu(gate_up[:K]) * gate_up[K:], w)."""
+    N, K = w.shape
+    _call("sq8_matmul_swiglu", _ptr(gate_up), _ptr(w), _ptr(scales), _ptr(y), N, K, group_size,
+          stream=stream)

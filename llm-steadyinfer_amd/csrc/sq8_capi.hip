@@ -4,6 +4,7 @@
 // layer.cpp:207-211) but reports a status code instead of aborting. Dispatch picks a kernel family
 // from the token count M and the alignment of the operands.
 #include "../../include/sq8.h"
+#include "../../include/sq8_decode.h"
 #include "sq8_common.h"
 
 namespace {
@@ -78,6 +79,39 @@ const char* sq8_status_string(int status) {
     case SQ8_ERR_DEVICE: return "no usable HIP device";
     default: return "unknown status";
   }
+}
+
+// Fused decode projections (include/sq8_decode.h): one token row through the VALU GEMV with its
+// input computed while staging. Only shapes that path takes are accepted.
+static int validate_fused(const void* x, const void* w, const void* s, const void* y, int N, int K,
+                          int gs) {
+  if (!x || !w || !s || !y) return SQ8_ERR_NULL;
+  if (N <= 0 || K <= 0 || K % 4 != 0 || !sq8::gemv_stream_fits(1, K)) return SQ8_ERR_DIMS;
+  if (gs <= 0 || !fast_shape(K, gs)) return SQ8_ERR_GROUP;
+  if (!aligned16(x) || !aligned16(w)) return SQ8_ERR_DIMS;
+  return SQ8_OK;
+}
+
+int sq8_matmul_rmsnorm(const float* x, const float* res, float* x_out, const float* norm_w,
+                       float eps, const int8_t* w, const float* scales, float* y, int N, int K,
+                       int group_size, void* hip_stream) {
+  const int v = validate_fused(x, w, scales, y, N, K, group_size);
+  if (v != SQ8_OK) return v;
+  if (!norm_w) return SQ8_ERR_NULL;
+  if (!aligned16(norm_w) || (res && !aligned16(res)) || (x_out && !aligned16(x_out)))
+    return SQ8_ERR_DIMS;
+  const hipError_t e = sq8::launch_gemv_norm(x, res, x_out, norm_w, eps, w, scales, y, N, K,
+                                             group_size, static_cast<hipStream_t>(hip_stream));
+  return e == hipSuccess ? SQ8_OK : SQ8_ERR_LAUNCH;
+}
+
+int sq8_matmul_swiglu(const float* gate_up, const int8_t* w, const float* scales, float* y, int N,
+                      int K, int group_size, void* hip_stream) {
+  const int v = validate_fused(gate_up, w, scales, y, N, K, group_size);
+  if (v != SQ8_OK) return v;
+  const hipError_t e = sq8::launch_gemv_swiglu(gate_up, w, scales, y, N, K, group_size,
+                                               static_cast<hipStream_t>(hip_stream));
+  return e == hipSuccess ? SQ8_OK : SQ8_ERR_LAUNCH;
 }
 
 const char* sq8_path_name(int M, int N, int K, int group_size) {

@@ -17,6 +17,11 @@ size_t mfma_workspace_bytes(int M, int N, int K);
 hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
                        int K, int gs, void* ws, hipStream_t st);
 bool gemv_stream_fits(int M, int K);
+hipError_t launch_gemv_norm(const float* x, const float* res, float* x_out, const float* nw,
+                            float eps, const int8_t* w, const float* s, float* y, int N, int K,
+                            int gs, hipStream_t st);
+hipError_t launch_gemv_swiglu(const float* ab, const int8_t* w, const float* s, float* y, int N,
+                              int K, int gs, hipStream_t st);
 hipError_t launch_generic(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
                           int K, int gs, hipStream_t st);
 

@@ -134,22 +134,85 @@ __global__ __launch_bounds__(kThreads) void gemv_rows_kernel(const float* __rest
 // U KiB per row, issuing all R x U dwordx4 loads of a step before using any of them. Latency is
 // hidden by residency (four 4-wave workgroups per CU) rather than by a second register set, which
 // keeps the register count low enough for that residency. TAIL: K is not a multiple of U KiB.
-template <int R, int U, int MT, int GS, bool TAIL, int WV = kWaves>
+// Optional work done while staging a single token row (M = 1), fusing the decode step's
+// elementwise layers into the projection that consumes them:
+//   kProNorm:   x' = x + res (res may be null), staged value rmsnorm(x') * nw; workgroup 0 also
+//               writes x' to x_out (may be null) as the new residual stream;
+//   kProSwiGLU: x holds [a | b] (2K values); staged value silu(a) * b.
+enum Prologue { kProNone = 0, kProNorm = 1, kProSwiGLU = 2 };
+// silu(a) * b as the reference's SwiGLU computes it (swiglu_kernel.cu:12-19).
+__device__ __forceinline__ float silu_mul(float a, float b) {
+  const float sig = 1.0f / (1.0f + expf(-a));
+  return (a * sig) * b;
+}
+struct ProArgs {
+  const float* res;
+  float* x_out;
+  const float* nw;
+  float eps;
+};
+
+template <int R, int U, int MT, int GS, bool TAIL, int WV = kWaves, int PRO = kProNone>
 __global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restrict__ x,
                                                          const int8_t* __restrict__ w,
                                                          const float* __restrict__ s,
                                                          float* __restrict__ y, int M, int N,
-                                                         int K, int gs_rt) {
+                                                         int K, int gs_rt, ProArgs pro = {}) {
   extern __shared__ float xs[];
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
   // Token rows M .. MT-1 are staged as zeros. float4 number i is stored at i ^ ((i >> 4) & 3): a
   // lane reads the 4 float4 of its 16-element chunk, and without the swizzle lanes l and l+4 would
   // hit the same LDS banks in every ds_read_b128 (4-way conflicts).
-  for (int i = tid; i < MT * K / 4; i += WV * kWave) {
-    const float4 v = i < M * K / 4 ? reinterpret_cast<const float4*>(x)[i]
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-    reinterpret_cast<float4*>(xs)[i ^ ((i >> 4) & 3)] = v;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  float4* xs4 = reinterpret_cast<float4*>(xs);
+  if (PRO == kProNone) {
+    for (int i = tid; i < MT * K / 4; i += WV * kWave) {
+      const float4 v = i < M * K / 4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      xs4[i ^ ((i >> 4) & 3)] = v;
+    }
+  } else if (PRO == kProNorm) {
+    __shared__ float red[WV];
+    const float4* r4 = reinterpret_cast<const float4*>(pro.res);
+    float ss = 0.f;
+    for (int i = tid; i < K / 4; i += WV * kWave) {
+      float4 v = x4[i];
+      if (r4) {
+        const float4 r = r4[i];
+        v = make_float4(v.x + r.x, v.y + r.y, v.z + r.z, v.w + r.w);
+      }
+      ss = fmaf(v.x, v.x, ss);
+      ss = fmaf(v.y, v.y, ss);
+      ss = fmaf(v.z, v.z, ss);
+      ss = fmaf(v.w, v.w, ss);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off /= 2) ss += __shfl_xor(ss, off, kWave);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float total = red[0];
+#pragma unroll
+    for (int v = 1; v < WV; ++v) total += red[v];
+    const float scale = rsqrtf(total / static_cast<float>(K) + pro.eps);
+    const float4* n4 = reinterpret_cast<const float4*>(pro.nw);
+    float4* o4 = reinterpret_cast<float4*>(pro.x_out);
+    for (int i = tid; i < K / 4; i += WV * kWave) {
+      float4 v = x4[i];
+      if (r4) {
+        const float4 r = r4[i];
+        v = make_float4(v.x + r.x, v.y + r.y, v.z + r.z, v.w + r.w);
+      }
+      if (o4 && blockIdx.x == 0) o4[i] = v;
+      const float4 g = n4[i];
+      xs4[i ^ ((i >> 4) & 3)] = make_float4(scale * v.x * g.x, scale * v.y * g.y,
+                                            scale * v.z * g.z, scale * v.w * g.w);
+    }
+  } else {
+    for (int i = tid; i < K / 4; i += WV * kWave) {
+      const float4 a = x4[i], b = x4[K / 4 + i];
+      xs4[i ^ ((i >> 4) & 3)] = make_float4(silu_mul(a.x, b.x), silu_mul(a.y, b.y),
+                                            silu_mul(a.z, b.z), silu_mul(a.w, b.w));
+    }
   }
   __syncthreads();
   const int nblk = (N + R - 1) / R;
@@ -296,43 +359,51 @@ namespace {
 constexpr size_t kStreamLdsMax = 64 * 1024;
 
 // WV waves per workgroup; 16 waves per CU in total, fewer when there are fewer row blocks.
-template <int R, int U, int MT, int GS, int WV>
+template <int R, int U, int MT, int GS, int WV, int PRO>
 hipError_t launch_sweep_t(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
-                          int K, int gs, hipStream_t st) {
+                          int K, int gs, const ProArgs& pro, hipStream_t st) {
   const size_t lds = static_cast<size_t>(MT) * K * sizeof(float);
   const int nblk = (N + R - 1) / R;
   const int grid = min((nblk + WV - 1) / WV, (16 / WV) * cu_count());
   if (K % (1024 * U) == 0) {
-    hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, false, WV>), dim3(grid), dim3(WV * kWave), lds,
-                       st, x, w, s, y, M, N, K, gs);
+    hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, false, WV, PRO>), dim3(grid), dim3(WV * kWave),
+                       lds, st, x, w, s, y, M, N, K, gs, pro);
   } else {
-    hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, true, WV>), dim3(grid), dim3(WV * kWave), lds,
-                       st, x, w, s, y, M, N, K, gs);
+    hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, true, WV, PRO>), dim3(grid), dim3(WV * kWave),
+                       lds, st, x, w, s, y, M, N, K, gs, pro);
   }
   return hipGetLastError();
 }
 
-template <int R, int U, int WV, int MT>
+template <int R, int U, int WV, int MT, int PRO = kProNone>
 hipError_t launch_sweep(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
-                        int K, int gs, hipStream_t st) {
-  return gs == 64 ? launch_sweep_t<R, U, MT, 64, WV>(x, w, s, y, M, N, K, gs, st)
-                  : launch_sweep_t<R, U, MT, 0, WV>(x, w, s, y, M, N, K, gs, st);
+                        int K, int gs, hipStream_t st, const ProArgs& pro = {}) {
+  return gs == 64 ? launch_sweep_t<R, U, MT, 64, WV, PRO>(x, w, s, y, M, N, K, gs, pro, st)
+                  : launch_sweep_t<R, U, MT, 0, WV, PRO>(x, w, s, y, M, N, K, gs, pro, st);
 }
 
-// Configurations measured best on the Llama-3-8B shapes. Rows under 8 KiB: 4 KiB per row per
-// step; up to 8192 rows one row per wave in 8-wave workgroups, more rows 2 rows per wave in
-// 4-wave workgroups. Longer rows: x fills up to 56 KiB of
-// LDS, so one 16-wave workgroup per CU, one row per wave and 7 KiB (or 2 KiB) per step keep
-// enough bytes in flight.
-template <int MT>
+// Configurations measured best on the Llama-3-8B and Qwen2-1.5B shapes. Rows of 8 KiB and more:
+// one row per wave; 7 KiB steps in 16-wave workgroups when K is a multiple of 7 KiB (Llama down,
+// 14 KiB rows), else 4 KiB steps in 8-wave workgroups (Qwen2 down, 8.75 KiB rows). Shorter rows:
+// a step covers the row in at most 4 iterations of 1 KiB, so short rows (1.5 KiB) do not issue
+// masked loads; up to 8192 rows one row per wave in 8-wave workgroups, more rows 2 rows per wave
+// in 4-wave workgroups.
+template <int MT, int PRO = kProNone>
 hipError_t launch_stream(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
-                         int K, int gs, hipStream_t st) {
+                         int K, int gs, hipStream_t st, const ProArgs& pro = {}) {
   if (K >= 8192) {
-    return K % 7168 == 0 ? launch_sweep<1, 7, 16, MT>(x, w, s, y, M, N, K, gs, st)
-                         : launch_sweep<1, 2, 16, MT>(x, w, s, y, M, N, K, gs, st);
+    return K % 7168 == 0 ? launch_sweep<1, 7, 16, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro)
+                         : launch_sweep<1, 4, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
   }
-  if (N <= 8192) return launch_sweep<1, 4, 8, MT>(x, w, s, y, M, N, K, gs, st);
-  return launch_sweep<2, 4, 4, MT>(x, w, s, y, M, N, K, gs, st);
+  const int u = K <= 1024 ? 1 : (K <= 2048 ? 2 : 4);
+  if (N <= 8192) {
+    if (u == 1) return launch_sweep<1, 1, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
+    if (u == 2) return launch_sweep<1, 2, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
+    return launch_sweep<1, 4, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
+  }
+  if (u == 1) return launch_sweep<2, 1, 4, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
+  if (u == 2) return launch_sweep<2, 2, 4, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
+  return launch_sweep<2, 4, 4, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
 }
 
 }  // namespace
@@ -368,6 +439,19 @@ hipError_t launch_generic(const float* x, const int8_t* w, const float* s, float
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+// Decode GEMV with a fused prologue (M = 1); the caller has validated the shape.
+hipError_t launch_gemv_norm(const float* x, const float* res, float* x_out, const float* nw,
+                            float eps, const int8_t* w, const float* s, float* y, int N, int K,
+                            int gs, hipStream_t st) {
+  const ProArgs pro{res, x_out, nw, eps};
+  return launch_stream<1, kProNorm>(x, w, s, y, 1, N, K, gs, st, pro);
+}
+
+hipError_t launch_gemv_swiglu(const float* ab, const int8_t* w, const float* s, float* y, int N,
+                              int K, int gs, hipStream_t st) {
+  return launch_stream<1, kProSwiGLU>(ab, w, s, y, 1, N, K, gs, st);
 }
 
 }  // namespace sq8

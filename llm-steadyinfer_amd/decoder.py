@@ -8,8 +8,11 @@ torch supplies device memory, streams and graph capture only. One decode step is
     O GEMV -> add + RMSNorm -> fused gate/up GEMV -> SwiGLU -> down GEMV
     -> add + final RMSNorm -> classifier GEMV -> argmax -> (pos, token) advance
 
-with the residual add of each block folded into the next RMSNorm. Positions and tokens live in
-device memory, so the step is captured once into a HIP graph and replayed per token.
+with the residual add of each block folded into the next RMSNorm. With ``fused=True`` (the
+default) every add + RMSNorm runs inside the prologue of the projection that consumes it
+(sq8_matmul_rmsnorm, the residual stream ping-ponging between two buffers) and SwiGLU inside the
+down projection's (sq8_matmul_swiglu): 6 launches per layer instead of 9. Positions and tokens
+live in device memory, so the step is captured once into a HIP graph and replayed per token.
 
 Weights come from an INT8 model file (model_file.py / the reference layout) or from an on-device
 random init of the same distribution (for benchmarks of the large shapes without writing a file).
@@ -22,7 +25,8 @@ from __future__ import annotations
 import numpy as np
 
 from . import (Workspace, add_rmsnorm, argmax, attention_decode, embedding, lib, matmul,
-               quantize, rmsnorm, rope_kv, rope_tables, step_advance, swiglu)
+               matmul_rmsnorm, matmul_swiglu, quantize, rmsnorm, rope_kv, rope_tables,
+               step_advance, swiglu)
 from .model_file import ModelConfig, ModelFile
 
 EPS = 1e-6
@@ -30,7 +34,7 @@ EPS = 1e-6
 
 class Int8Decoder:
     def __init__(self, cfg: ModelConfig, weights: dict, group_size: int, max_seq: int,
-                 device="cuda"):
+                 device="cuda", fused: bool = True):
         import torch
         self.torch = torch
         self.cfg, self.gs, self.max_seq, self.device = cfg, group_size, max_seq, device
@@ -45,7 +49,9 @@ class Int8Decoder:
         self.sin = torch.empty((max_seq, self.hs), **f32)
         self.cos = torch.empty((max_seq, self.hs), **f32)
         rope_tables(self.sin, self.cos, self.hs, max_seq, float(cfg.rope_theta))
+        self.fused = fused
         self.x = torch.zeros(d, **f32)        # residual stream
+        self.x2 = torch.zeros(d, **f32)       # its other half when the norms are fused
         self.xn = torch.zeros(d, **f32)       # normalised input of the next projection
         self.qkv = torch.zeros(d + 2 * kv, **f32)
         self.att = torch.zeros(d, **f32)
@@ -63,7 +69,7 @@ class Int8Decoder:
 
     # ------------------------------------------------------------------ construction
     @classmethod
-    def from_file(cls, path, max_seq: int, device="cuda") -> "Int8Decoder":
+    def from_file(cls, path, max_seq: int, device="cuda", fused: bool = True) -> "Int8Decoder":
         """Load an INT8 model file (reference layout) and upload fused projections."""
         import torch
         m = ModelFile(path)
@@ -86,11 +92,11 @@ class Int8Decoder:
              "emb": dev(m.fp32("embedding"), torch.float32),
              "norm": [dev(m.fp32("rmsnorm", i).reshape(-1), torch.float32)
                       for i in range(2 * L + 1)]}
-        return cls(cfg, w, gs, max_seq, device)
+        return cls(cfg, w, gs, max_seq, device, fused)
 
     @classmethod
     def random(cls, cfg: ModelConfig, max_seq: int, group_size: int = 64, seed: int = 0,
-               w_std: float = 0.02, device="cuda") -> "Int8Decoder":
+               w_std: float = 0.02, device="cuda", fused: bool = True) -> "Int8Decoder":
         """Random-init model on the device: projections ~ N(0, w_std) quantised per group by
         sq8_quantize (bit-identical to the model-file quantiser), embedding ~ N(0, 1), unit norms."""
         import torch
@@ -115,7 +121,7 @@ class Int8Decoder:
              "emb": torch.randn((cfg.vocab, d), generator=gen, dtype=torch.float32, device=device),
              "norm": [torch.ones(d, dtype=torch.float32, device=device) for _ in range(2 * L + 1)]}
         torch.cuda.synchronize()
-        return cls(cfg, w, group_size, max_seq, device)
+        return cls(cfg, w, group_size, max_seq, device, fused)
 
     def weight_bytes(self) -> int:
         """Bytes of weights one decode step reads (int8 + scales of every projection)."""
@@ -132,6 +138,44 @@ class Int8Decoder:
         matmul(x, q, s, y, group_size=self.gs, workspace=self.ws, stream=stream)
 
     def _launch_step(self, stream, want_logits: bool = True):
+        if self.fused:
+            self._launch_step_fused(stream, want_logits)
+        else:
+            self._launch_step_plain(stream, want_logits)
+
+    def _mm_norm(self, x, res, x_out, norm, qs, y, stream):
+        q, s = qs
+        matmul_rmsnorm(x, res, x_out, norm, q, s, y, self.gs, EPS, stream=stream)
+
+    def _launch_step_fused(self, stream, want_logits: bool):
+        cfg = self.cfg
+        L, d, kv = cfg.layer_num, cfg.dim, self.kv_dim
+        w = self.w
+        cur, other = self.x, self.x2
+        embedding(w["emb"], self.token, cur, stream=stream)
+        for l in range(L):
+            if l == 0:
+                self._mm_norm(cur, None, None, w["norm"][0], w["qkv"][0], self.qkv, stream)
+            else:
+                self._mm_norm(cur, self.proj, other, w["norm"][l], w["qkv"][l], self.qkv, stream)
+                cur, other = other, cur
+            rope_kv(self.qkv, d, kv, self.hs, self.pos, self.sin, self.cos, self.kcache[l],
+                    self.vcache[l], self.max_seq, stream=stream)
+            attention_decode(self.qkv[:d], self.kcache[l], self.vcache[l], self.pos, self.att,
+                             cfg.head_num, cfg.kv_head_num, self.hs, self.max_seq, stream=stream)
+            self._mm(self.att, w["o"][l], self.proj, stream)
+            self._mm_norm(cur, self.proj, other, w["norm"][L + l], w["gu"][l], self.gu, stream)
+            cur, other = other, cur
+            q, s = w["down"][l]
+            matmul_swiglu(self.gu, q, s, self.proj, self.gs, stream=stream)
+        if want_logits:
+            self._mm_norm(cur, self.proj, None, w["norm"][2 * L], w["cls"], self.logits, stream)
+            argmax(self.logits, self.next, workspace=self.argmax_ws, stream=stream)
+            step_advance(self.pos, self.token, self.next, stream=stream)
+        else:
+            step_advance(self.pos, self.token, self.token, stream=stream)
+
+    def _launch_step_plain(self, stream, want_logits: bool):
         """Enqueue one token: reads self.token / self.pos, writes self.next (when want_logits)
         and advances pos (and token = next)."""
         cfg = self.cfg

@@ -26,6 +26,10 @@ def test_decode_ops_reject_bad_arguments(sq8):
     assert L.sq8_swiglu(FAKE, None, FAKE, 4, None) == sq8.SQ8_ERR_NULL
     assert L.sq8_embedding(FAKE, 0, 8, FAKE, 1, FAKE, None) == sq8.SQ8_ERR_DIMS
     assert L.sq8_step_advance(FAKE, None, FAKE, None) == sq8.SQ8_ERR_NULL
+    assert L.sq8_matmul_rmsnorm(FAKE, None, None, None, 1e-6, FAKE, FAKE, FAKE, 8, 64, 64, None) == sq8.SQ8_ERR_NULL
+    assert L.sq8_matmul_rmsnorm(FAKE, None, None, FAKE, 1e-6, FAKE, FAKE, FAKE, 8, 20000, 16, None) == sq8.SQ8_ERR_DIMS
+    assert L.sq8_matmul_swiglu(FAKE, FAKE, FAKE, FAKE, 8, 96, 64, None) == sq8.SQ8_ERR_GROUP
+    assert L.sq8_matmul_swiglu(FAKE + 4, FAKE, FAKE, FAKE, 8, 128, 64, None) == sq8.SQ8_ERR_DIMS
 
 
 def _t(a, dev, dtype=None):
@@ -177,3 +181,44 @@ def test_step_advance(sq8, dev):
     nxt = torch.tensor([977], dtype=torch.int32, device=dev)
     sq8.step_advance(pos, tok, nxt)
     assert int(pos.item()) == 42 and int(tok.item()) == 977
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K,with_res", [(2048, 1536, False), (17920, 1536, True), (151936, 1536, True),
+                                          (6144, 4096, True), (96, 256, True)])
+def test_matmul_rmsnorm_equals_separate_ops(sq8, dev, N, K, with_res):
+    """The fused prologue gives the unfused add + RMSNorm + GEMV result (both against the oracle)
+    and writes the residual stream once."""
+    import torch
+    rng = np.random.default_rng(N + K)
+    x = (rng.standard_normal(K) * 2).astype(np.float32)
+    r = rng.standard_normal(K).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    _, q, s = o.make_case(1, N, K, 64, seed=K)
+    qt, st = _t(q, dev), _t(s, dev)
+    y = torch.empty(N, device=dev)
+    xo = torch.full((K,), 9.0, device=dev)
+    sq8.matmul_rmsnorm(_t(x, dev), _t(r, dev) if with_res else None, xo, _t(g, dev), qt, st, y)
+    xin = (x + r) if with_res else x
+    xn = do.rmsnorm(xin, g).astype(np.float32)
+    ref = o.matmul_f64(xn.reshape(1, -1), q, s, 64).reshape(-1)
+    elem, norm = o.rel_errors(y.cpu().numpy().reshape(1, -1), ref.reshape(1, -1))
+    print(f"fused norm N={N} K={K}: elem {elem:.2e} norm {norm:.2e}")
+    assert elem <= 1e-3 and norm <= 1e-5
+    np.testing.assert_array_equal(xo.cpu().numpy(), xin)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N,K", [(1536, 8960), (4096, 14336), (64, 1024)])
+def test_matmul_swiglu_equals_separate_ops(sq8, dev, N, K):
+    import torch
+    rng = np.random.default_rng(K)
+    ab = (rng.standard_normal(2 * K) * 3).astype(np.float32)
+    _, q, s = o.make_case(1, N, K, 64, seed=N)
+    y = torch.empty(N, device=dev)
+    sq8.matmul_swiglu(_t(ab, dev), _t(q, dev), _t(s, dev), y)
+    h = do.swiglu(ab[:K], ab[K:]).astype(np.float32)
+    ref = o.matmul_f64(h.reshape(1, -1), q, s, 64)
+    elem, norm = o.rel_errors(y.cpu().numpy().reshape(1, -1), ref)
+    print(f"fused swiglu N={N} K={K}: elem {elem:.2e} norm {norm:.2e}")
+    assert elem <= 1e-3 and norm <= 1e-5

@@ -33,10 +33,11 @@ def test_greedy_tokens_match_oracle(dev, tmp_path, cfg, seed):
     ref_tokens, ref_logits = do.DecodeModel(mf.ModelFile(path), max_seq=64).generate(prompt, 24)
     gaps = [float(np.sort(lg)[-1] - np.sort(lg)[-2]) for lg in ref_logits]
     print("oracle tokens", ref_tokens, "min top-2 gap", min(gaps))
-    D = _decoder_mod().Int8Decoder.from_file(path, max_seq=64, device=dev)
-    eager = D.generate(prompt, 24, use_graph=False)
-    print("eager tokens ", eager)
-    assert eager == ref_tokens
+    for fused in (True, False):
+        D = _decoder_mod().Int8Decoder.from_file(path, max_seq=64, device=dev, fused=fused)
+        eager = D.generate(prompt, 24, use_graph=False)
+        print("eager tokens ", eager, "fused" if fused else "separate ops")
+        assert eager == ref_tokens
 
 
 @pytest.mark.gpu
@@ -56,13 +57,14 @@ def test_graph_replay_matches_eager(dev, tmp_path):
 
 
 @pytest.mark.gpu
-def test_logits_match_oracle_at_each_step(dev, tmp_path):
+@pytest.mark.parametrize("fused", [True, False])
+def test_logits_match_oracle_at_each_step(dev, tmp_path, fused):
     """Beyond token identity: the classifier logits of every step agree with the oracle to
     fp32 accuracy (max error / max |logit| <= 1e-4)."""
     import torch
     path = mf.write_random(tmp_path / "m.bin", TINY, 64, seed=5, w_std=0.2)
     ref = do.DecodeModel(mf.ModelFile(path), max_seq=64)
-    D = _decoder_mod().Int8Decoder.from_file(path, max_seq=64, device=dev)
+    D = _decoder_mod().Int8Decoder.from_file(path, max_seq=64, device=dev, fused=fused)
     D.reset()
     stream = torch.cuda.current_stream()
     tok = 17
