@@ -61,6 +61,14 @@ int sq8_attention_decode(const float* q, const float* key_cache, const float* va
                          const int32_t* pos, float* out, int head_num, int kv_head_num,
                          int head_size, int max_seq, void* hip_stream);
 
+/* sq8_rope_kv followed by sq8_attention_decode in one launch: reads q, k, v from the projection
+ * output qkv = [q (head_num*head_size) | k | v] of the token at *pos, rotates q and k, writes the
+ * rotated k and v to row *pos of the caches and returns the attention output in out. */
+int sq8_rope_attention_decode(const float* qkv, int head_num, int kv_head_num, int head_size,
+                              const int32_t* pos, const float* sin_cache, const float* cos_cache,
+                              float* key_cache, float* value_cache, float* out, int max_seq,
+                              void* hip_stream);
+
 /* out[i] = silu(a[i]) * b[i], silu(v) = v / (1 + exp(-v)) (swiglu_kernel_cu_fp32,
  * src/source/op/kernels/cuda/swiglu_kernel.cu:4-21). `out` may alias `a`. */
 int sq8_swiglu(const float* a, const float* b, float* out, int n, void* hip_stream);

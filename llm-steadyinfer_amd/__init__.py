@@ -26,7 +26,7 @@ EXPORTED_SYMBOLS = ("sq8_matmul", "sq8_workspace_bytes", "sq8_status_string", "s
 DECODE_SYMBOLS = ("sq8_embedding", "sq8_rmsnorm", "sq8_add_rmsnorm", "sq8_rope_tables", "sq8_rope_kv",
                   "sq8_attention_decode", "sq8_swiglu", "sq8_add", "sq8_argmax_workspace_bytes",
                   "sq8_argmax", "sq8_quantize", "sq8_step_advance", "sq8_matmul_rmsnorm",
-                  "sq8_matmul_swiglu")
+                  "sq8_matmul_swiglu", "sq8_rope_attention_decode")
 
 _lib = None
 
@@ -69,6 +69,7 @@ def lib() -> ctypes.CDLL:
             "sq8_step_advance": [vp, vp, vp, vp],
             "sq8_matmul_rmsnorm": [vp, vp, vp, vp, f32, vp, vp, vp, I, I, I, vp],
             "sq8_matmul_swiglu": [vp, vp, vp, vp, I, I, I, vp],
+            "sq8_rope_attention_decode": [vp, I, I, I, vp, vp, vp, vp, vp, vp, I, vp],
         }
         for name, args in sigs.items():
             fn = getattr(L, name)
@@ -237,4 +238,12 @@ def matmul_swiglu(gate_up, w, scales, y, group_size: int = 64, stream=None):
     """y = matmul(silu(gate_up[:K]) * gate_up[K:], w)."""
     N, K = w.shape
     _call("sq8_matmul_swiglu", _ptr(gate_up), _ptr(w), _ptr(scales), _ptr(y), N, K, group_size,
+          stream=stream)
+
+
+def rope_attention_decode(qkv, head_num: int, kv_head_num: int, head_size: int, pos, sin_cache,
+                          cos_cache, kcache, vcache, out, max_seq: int, stream=None):
+    """RoPE on the token's q and k, cache write at *pos and attention, in one launch."""
+    _call("sq8_rope_attention_decode", _ptr(qkv), head_num, kv_head_num, head_size, _ptr(pos),
+          _ptr(sin_cache), _ptr(cos_cache), _ptr(kcache), _ptr(vcache), _ptr(out), max_seq,
           stream=stream)

@@ -134,36 +134,85 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, int dim, int kv_dim, int
 }
 
 // One workgroup per query head.
+//  * ROPE (fused RoPE + cache write): q and the kv head's k are rotated here from the projection
+//    output qkv = [q | k | v]; the first query head of each kv group writes k and v to cache row
+//    pos, and every head uses its own rotated copies for position pos (so no workgroup reads a
+//    row another one is writing). Without ROPE, q is read as given and row pos from the cache.
 //  * Scores: thread t owns cache position t (t, t + 256, ...) and reads its key row as float4
 //    loads that are all independent (one memory round trip per 256 positions); q is broadcast from
 //    LDS.
 //  * Softmax over the scores in LDS: workgroup max and sum (fixed order).
-//  * Values: wave w takes positions w, w + 4, ... and lane l the dims l, l + 64, ...; four
-//    positions per iteration keep four independent loads in flight; the four waves' partial sums
+//  * Values: wave w takes positions w, w + 4, ... and lane l the dims l, l + 64, ...; eight
+//    positions per iteration keep eight independent loads in flight; the four waves' partial sums
 //    meet in LDS in wave order.
-template <int HS_MAX>
+struct RopeArgs {
+  int dim, kv_dim;
+  const float* sin_cache;
+  const float* cos_cache;
+  float* kcache_w;
+  float* vcache_w;
+};
+
+template <int HS_MAX, bool ROPE>
 __global__ __launch_bounds__(kBlock) void attention_decode_kernel(
     const float* __restrict__ q, const float* __restrict__ kcache,
     const float* __restrict__ vcache, const int32_t* __restrict__ pos_ptr,
-    float* __restrict__ out, int head_num, int kv_head_num, int head_size) {
+    float* __restrict__ out, int head_num, int kv_head_num, int head_size, RopeArgs ra) {
   extern __shared__ float s_p[];  // [seq] scores, then probabilities
   __shared__ float red[kBlockWaves];
   __shared__ __attribute__((aligned(16))) float s_q[HS_MAX];
+  __shared__ float s_k[HS_MAX];
+  __shared__ float s_v[HS_MAX];
   __shared__ float s_part[kBlockWaves][HS_MAX];
   constexpr int DPL = HS_MAX / kWave;  // head dims per lane in the value pass
   const int head = blockIdx.x;
-  const int seq = *pos_ptr + 1;
+  const int pos = *pos_ptr;
+  const int seq = pos + 1;
   const int kv_dim = kv_head_num * head_size;
-  const int hoff = (head * kv_head_num / head_num) * head_size;
+  const int group = head * kv_head_num / head_num;
+  const int hoff = group * head_size;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
-  for (int d = threadIdx.x; d < head_size; d += kBlock) s_q[d] = q[head * head_size + d];
+  // Positions read from the cache: all of them, or all but pos when pos comes from registers.
+  const int ncache = ROPE ? pos : seq;
+  if (ROPE) {
+    const int half = head_size / 2;
+    const bool leader = head == (group * head_num + kv_head_num - 1) / kv_head_num;
+    for (int i = threadIdx.x; i < half; i += kBlock) {
+      const float fci = ra.sin_cache[static_cast<size_t>(pos) * head_size + 2 * i];
+      const float fcr = ra.cos_cache[static_cast<size_t>(pos) * head_size + 2 * i];
+      const float* qh = q + head * head_size;
+      const float q0 = qh[i], q1 = qh[i + half];
+      s_q[i] = fcr * q0 - fci * q1;
+      s_q[i + half] = fcr * q1 + fci * q0;
+      const float* kh = q + ra.dim + hoff;
+      const float k0 = kh[i], k1 = kh[i + half];
+      const float r0 = fcr * k0 - fci * k1, r1 = fcr * k1 + fci * k0;
+      s_k[i] = r0;
+      s_k[i + half] = r1;
+      const float* vh = q + ra.dim + ra.kv_dim + hoff;
+      s_v[i] = vh[i];
+      s_v[i + half] = vh[i + half];
+      if (leader) {
+        float* krow = ra.kcache_w + static_cast<size_t>(pos) * kv_dim + hoff;
+        float* vrow = ra.vcache_w + static_cast<size_t>(pos) * kv_dim + hoff;
+        krow[i] = r0;
+        krow[i + half] = r1;
+        vrow[i] = vh[i];
+        vrow[i + half] = vh[i + half];
+      }
+    }
+  } else {
+    for (int d = threadIdx.x; d < head_size; d += kBlock) s_q[d] = q[head * head_size + d];
+  }
   __syncthreads();
   const float scale = 1.f / sqrtf(static_cast<float>(head_size));
   const bool vec4 = (head_size % 4) == 0 && (kv_dim % 4) == 0 && (hoff % 4) == 0;
   for (int t = threadIdx.x; t < seq; t += kBlock) {
-    const float* krow = kcache + static_cast<size_t>(t) * kv_dim + hoff;
     float a0 = 0.f, a1 = 0.f;
-    if (vec4) {
+    if (ROPE && t == pos) {
+      for (int d = 0; d < head_size; ++d) a0 = fmaf(s_q[d], s_k[d], a0);
+    } else if (vec4) {
+      const float* krow = kcache + static_cast<size_t>(t) * kv_dim + hoff;
 #pragma unroll 4
       for (int d = 0; d < head_size; d += 8) {
         const float4 k0 = *reinterpret_cast<const float4*>(krow + d);
@@ -182,6 +231,7 @@ __global__ __launch_bounds__(kBlock) void attention_decode_kernel(
         }
       }
     } else {
+      const float* krow = kcache + static_cast<size_t>(t) * kv_dim + hoff;
       for (int d = 0; d < head_size; ++d) a0 = fmaf(s_q[d], krow[d], a0);
     }
     s_p[t] = (a0 + a1) * scale;
@@ -201,29 +251,36 @@ __global__ __launch_bounds__(kBlock) void attention_decode_kernel(
 #pragma unroll
   for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
   const float* vbase = vcache + hoff + lane;
+  constexpr int UNR = 8;
   int t = wave;
-  for (; t + 3 * kBlockWaves < seq; t += 4 * kBlockWaves) {
-    float v[4][DPL];
+  for (; t + (UNR - 1) * kBlockWaves < ncache; t += UNR * kBlockWaves) {
+    float v[UNR][DPL];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < UNR; ++u)
 #pragma unroll
       for (int j = 0; j < DPL; ++j)
         v[u][j] = lane + j * kWave < head_size
                       ? vbase[static_cast<size_t>(t + u * kBlockWaves) * kv_dim + j * kWave]
                       : 0.f;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < UNR; ++u) {
       const float p = s_p[t + u * kBlockWaves];
 #pragma unroll
       for (int j = 0; j < DPL; ++j) acc[j] = fmaf(p, v[u][j], acc[j]);
     }
   }
-  for (; t < seq; t += kBlockWaves) {
+  for (; t < ncache; t += kBlockWaves) {
     const float p = s_p[t];
 #pragma unroll
     for (int j = 0; j < DPL; ++j)
       if (lane + j * kWave < head_size)
         acc[j] = fmaf(p, vbase[static_cast<size_t>(t) * kv_dim + j * kWave], acc[j]);
+  }
+  if (ROPE && wave == pos % kBlockWaves) {  // position pos from registers, in its wave's order
+    const float p = s_p[pos];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j)
+      if (lane + j * kWave < head_size) acc[j] = fmaf(p, s_v[lane + j * kWave], acc[j]);
   }
 #pragma unroll
   for (int j = 0; j < DPL; ++j) s_part[wave][lane + j * kWave] = acc[j];
@@ -439,9 +496,28 @@ int sq8_attention_decode(const float* q, const float* key_cache, const float* va
     return SQ8_ERR_DIMS;
   const size_t lds = static_cast<size_t>(max_seq) * sizeof(float);
   if (lds > 64 * 1024) return SQ8_ERR_DIMS;  // scores of one head live in LDS
-  hipLaunchKernelGGL((attention_decode_kernel<256>), dim3(head_num), dim3(kBlock), lds,
+  hipLaunchKernelGGL((attention_decode_kernel<256, false>), dim3(head_num), dim3(kBlock), lds,
                      stream_of(hip_stream), q, key_cache, value_cache, pos, out, head_num,
-                     kv_head_num, head_size);
+                     kv_head_num, head_size, RopeArgs{});
+  return launched();
+}
+
+int sq8_rope_attention_decode(const float* qkv, int head_num, int kv_head_num, int head_size,
+                              const int32_t* pos, const float* sin_cache, const float* cos_cache,
+                              float* key_cache, float* value_cache, float* out, int max_seq,
+                              void* hip_stream) {
+  if (!qkv || !pos || !sin_cache || !cos_cache || !key_cache || !value_cache || !out)
+    return SQ8_ERR_NULL;
+  if (head_num <= 0 || kv_head_num <= 0 || head_num % kv_head_num || head_size <= 0 ||
+      head_size % 2 || head_size > 256 || max_seq <= 0)
+    return SQ8_ERR_DIMS;
+  const size_t lds = static_cast<size_t>(max_seq) * sizeof(float);
+  if (lds > 64 * 1024) return SQ8_ERR_DIMS;
+  const RopeArgs ra{head_num * head_size, kv_head_num * head_size, sin_cache, cos_cache, key_cache,
+                    value_cache};
+  hipLaunchKernelGGL((attention_decode_kernel<256, true>), dim3(head_num), dim3(kBlock), lds,
+                     stream_of(hip_stream), qkv, key_cache, value_cache, pos, out, head_num,
+                     kv_head_num, head_size, ra);
   return launched();
 }
 

@@ -10,8 +10,9 @@ torch supplies device memory, streams and graph capture only. One decode step is
 
 with the residual add of each block folded into the next RMSNorm. With ``fused=True`` (the
 default) every add + RMSNorm runs inside the prologue of the projection that consumes it
-(sq8_matmul_rmsnorm, the residual stream ping-ponging between two buffers) and SwiGLU inside the
-down projection's (sq8_matmul_swiglu): 6 launches per layer instead of 9. Positions and tokens
+(sq8_matmul_rmsnorm, the residual stream ping-ponging between two buffers), SwiGLU inside the
+down projection's (sq8_matmul_swiglu) and RoPE + cache write inside attention
+(sq8_rope_attention_decode): 5 launches per layer instead of 9. Positions and tokens
 live in device memory, so the step is captured once into a HIP graph and replayed per token.
 
 Weights come from an INT8 model file (model_file.py / the reference layout) or from an on-device
@@ -25,8 +26,8 @@ from __future__ import annotations
 import numpy as np
 
 from . import (Workspace, add_rmsnorm, argmax, attention_decode, embedding, lib, matmul,
-               matmul_rmsnorm, matmul_swiglu, quantize, rmsnorm, rope_kv, rope_tables,
-               step_advance, swiglu)
+               matmul_rmsnorm, matmul_swiglu, quantize, rmsnorm, rope_attention_decode, rope_kv,
+               rope_tables, step_advance, swiglu)
 from .model_file import ModelConfig, ModelFile
 
 EPS = 1e-6
@@ -159,10 +160,9 @@ class Int8Decoder:
             else:
                 self._mm_norm(cur, self.proj, other, w["norm"][l], w["qkv"][l], self.qkv, stream)
                 cur, other = other, cur
-            rope_kv(self.qkv, d, kv, self.hs, self.pos, self.sin, self.cos, self.kcache[l],
-                    self.vcache[l], self.max_seq, stream=stream)
-            attention_decode(self.qkv[:d], self.kcache[l], self.vcache[l], self.pos, self.att,
-                             cfg.head_num, cfg.kv_head_num, self.hs, self.max_seq, stream=stream)
+            rope_attention_decode(self.qkv, cfg.head_num, cfg.kv_head_num, self.hs, self.pos,
+                                  self.sin, self.cos, self.kcache[l], self.vcache[l], self.att,
+                                  self.max_seq, stream=stream)
             self._mm(self.att, w["o"][l], self.proj, stream)
             self._mm_norm(cur, self.proj, other, w["norm"][L + l], w["gu"][l], self.gu, stream)
             cur, other = other, cur

@@ -222,3 +222,36 @@ def test_matmul_swiglu_equals_separate_ops(sq8, dev, N, K):
     elem, norm = o.rel_errors(y.cpu().numpy().reshape(1, -1), ref)
     print(f"fused swiglu N={N} K={K}: elem {elem:.2e} norm {norm:.2e}")
     assert elem <= 1e-3 and norm <= 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads,kv_heads,hs,pos", [(12, 2, 128, 0), (12, 2, 128, 77), (32, 8, 128, 300),
+                                                   (4, 4, 64, 9)])
+def test_rope_attention_equals_separate_ops(sq8, dev, heads, kv_heads, hs, pos):
+    """The fused launch writes the same cache row and returns the same output as sq8_rope_kv
+    followed by sq8_attention_decode (both against the oracle)."""
+    import torch
+    max_seq = 512
+    dim, kv = heads * hs, kv_heads * hs
+    rng = np.random.default_rng(pos + heads)
+    qkv = rng.standard_normal(dim + 2 * kv).astype(np.float32)
+    kc0 = rng.standard_normal((max_seq, kv)).astype(np.float32)
+    vc0 = rng.standard_normal((max_seq, kv)).astype(np.float32)
+    sin = torch.empty((max_seq, hs), device=dev)
+    cos = torch.empty((max_seq, hs), device=dev)
+    sq8.rope_tables(sin, cos, hs, max_seq, 1e6)
+    p = _t(np.array([pos], np.int32), dev)
+    kc, vc, out = _t(kc0, dev), _t(vc0, dev), torch.empty(dim, device=dev)
+    sq8.rope_attention_decode(_t(qkv, dev), heads, kv_heads, hs, p, sin, cos, kc, vc, out, max_seq)
+    kc2, vc2, out2 = _t(kc0, dev), _t(vc0, dev), torch.empty(dim, device=dev)
+    q2 = _t(qkv, dev)
+    sq8.rope_kv(q2, dim, kv, hs, p, sin, cos, kc2, vc2, max_seq)
+    sq8.attention_decode(q2[:dim], kc2, vc2, p, out2, heads, kv_heads, hs, max_seq)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(kc.cpu().numpy(), kc2.cpu().numpy())
+    np.testing.assert_array_equal(vc.cpu().numpy(), vc2.cpu().numpy())
+    s_np, c_np = sin.cpu().numpy().astype(np.float64), cos.cpu().numpy().astype(np.float64)
+    qr = do.rope(qkv[:dim], heads, hs, pos, s_np, c_np)
+    ref = do.attention(qr, kc2.cpu().numpy(), vc2.cpu().numpy(), pos, heads, kv_heads, hs)
+    _close(out.cpu().numpy(), ref, 2e-6, "fused rope+attention")
+    _close(out2.cpu().numpy(), ref, 2e-6, "separate")
