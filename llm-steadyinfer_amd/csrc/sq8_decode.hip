@@ -29,7 +29,8 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// Sum over the workgroup (kBlock threads); every thread gets the total. `red` holds kBlockWaves.
+// Sum over a workgroup of W waves; every thread gets the total. `red` holds W floats.
+template <int W = kBlockWaves>
 __device__ __forceinline__ float block_sum(float v, float* red) {
   v = wave_sum(v);
   const int wave = threadIdx.x >> 6;
@@ -38,10 +39,11 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   __syncthreads();
   float t = red[0];
 #pragma unroll
-  for (int i = 1; i < kBlockWaves; ++i) t += red[i];
+  for (int i = 1; i < W; ++i) t += red[i];
   return t;
 }
 
+template <int W = kBlockWaves>
 __device__ __forceinline__ float block_max(float v, float* red) {
   v = wave_max(v);
   const int wave = threadIdx.x >> 6;
@@ -50,7 +52,7 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   __syncthreads();
   float t = red[0];
 #pragma unroll
-  for (int i = 1; i < kBlockWaves; ++i) t = fmaxf(t, red[i]);
+  for (int i = 1; i < W; ++i) t = fmaxf(t, red[i]);
   return t;
 }
 
@@ -138,13 +140,13 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, int dim, int kv_dim, int
 //    output qkv = [q | k | v]; the first query head of each kv group writes k and v to cache row
 //    pos, and every head uses its own rotated copies for position pos (so no workgroup reads a
 //    row another one is writing). Without ROPE, q is read as given and row pos from the cache.
-//  * Scores: thread t owns cache position t (t, t + 256, ...) and reads its key row as float4
-//    loads that are all independent (one memory round trip per 256 positions); q is broadcast from
-//    LDS.
+//  * Scores: thread t owns cache position t (t, t + 1024, ...) and reads its key row as float4
+//    loads that are all independent (one memory round trip per 1024 positions); q is broadcast
+//    from LDS.
 //  * Softmax over the scores in LDS: workgroup max and sum (fixed order).
-//  * Values: wave w takes positions w, w + 4, ... and lane l the dims l, l + 64, ...; eight
-//    positions per iteration keep eight independent loads in flight; the four waves' partial sums
-//    meet in LDS in wave order.
+//  * Values: wave w of 16 takes positions w, w + 16, ... and lane l the dims l, l + 64, ...;
+//    eight positions per iteration keep eight independent loads in flight; the 16 waves' partial
+//    sums meet in LDS in wave order.
 struct RopeArgs {
   int dim, kv_dim;
   const float* sin_cache;
@@ -153,17 +155,20 @@ struct RopeArgs {
   float* vcache_w;
 };
 
+constexpr int kAttnBlock = 1024;
+constexpr int kAttnWaves = kAttnBlock / kWave;
+
 template <int HS_MAX, bool ROPE>
-__global__ __launch_bounds__(kBlock) void attention_decode_kernel(
+__global__ __launch_bounds__(kAttnBlock) void attention_decode_kernel(
     const float* __restrict__ q, const float* __restrict__ kcache,
     const float* __restrict__ vcache, const int32_t* __restrict__ pos_ptr,
     float* __restrict__ out, int head_num, int kv_head_num, int head_size, RopeArgs ra) {
   extern __shared__ float s_p[];  // [seq] scores, then probabilities
-  __shared__ float red[kBlockWaves];
+  __shared__ float red[kAttnWaves];
   __shared__ __attribute__((aligned(16))) float s_q[HS_MAX];
   __shared__ float s_k[HS_MAX];
   __shared__ float s_v[HS_MAX];
-  __shared__ float s_part[kBlockWaves][HS_MAX];
+  __shared__ float s_part[kAttnWaves][HS_MAX];
   constexpr int DPL = HS_MAX / kWave;  // head dims per lane in the value pass
   const int head = blockIdx.x;
   const int pos = *pos_ptr;
@@ -177,7 +182,7 @@ __global__ __launch_bounds__(kBlock) void attention_decode_kernel(
   if (ROPE) {
     const int half = head_size / 2;
     const bool leader = head == (group * head_num + kv_head_num - 1) / kv_head_num;
-    for (int i = threadIdx.x; i < half; i += kBlock) {
+    for (int i = threadIdx.x; i < half; i += kAttnBlock) {
       const float fci = ra.sin_cache[static_cast<size_t>(pos) * head_size + 2 * i];
       const float fcr = ra.cos_cache[static_cast<size_t>(pos) * head_size + 2 * i];
       const float* qh = q + head * head_size;
@@ -202,18 +207,18 @@ __global__ __launch_bounds__(kBlock) void attention_decode_kernel(
       }
     }
   } else {
-    for (int d = threadIdx.x; d < head_size; d += kBlock) s_q[d] = q[head * head_size + d];
+    for (int d = threadIdx.x; d < head_size; d += kAttnBlock) s_q[d] = q[head * head_size + d];
   }
   __syncthreads();
   const float scale = 1.f / sqrtf(static_cast<float>(head_size));
   const bool vec4 = (head_size % 4) == 0 && (kv_dim % 4) == 0 && (hoff % 4) == 0;
-  for (int t = threadIdx.x; t < seq; t += kBlock) {
+  for (int t = threadIdx.x; t < seq; t += kAttnBlock) {
     float a0 = 0.f, a1 = 0.f;
     if (ROPE && t == pos) {
       for (int d = 0; d < head_size; ++d) a0 = fmaf(s_q[d], s_k[d], a0);
     } else if (vec4) {
       const float* krow = kcache + static_cast<size_t>(t) * kv_dim + hoff;
-#pragma unroll 4
+#pragma unroll 8
       for (int d = 0; d < head_size; d += 8) {
         const float4 k0 = *reinterpret_cast<const float4*>(krow + d);
         const float4 q0 = *reinterpret_cast<const float4*>(s_q + d);
@@ -238,45 +243,45 @@ __global__ __launch_bounds__(kBlock) void attention_decode_kernel(
   }
   __syncthreads();
   float m = -FLT_MAX;
-  for (int t = threadIdx.x; t < seq; t += kBlock) m = fmaxf(m, s_p[t]);
-  m = block_max(m, red);
+  for (int t = threadIdx.x; t < seq; t += kAttnBlock) m = fmaxf(m, s_p[t]);
+  m = block_max<kAttnWaves>(m, red);
   float l = 0.f;
-  for (int t = threadIdx.x; t < seq; t += kBlock) {
+  for (int t = threadIdx.x; t < seq; t += kAttnBlock) {
     const float p = expf(s_p[t] - m);
     s_p[t] = p;
     l += p;
   }
-  l = block_sum(l, red);  // its barriers also publish the probabilities
+  l = block_sum<kAttnWaves>(l, red);  // its barriers also publish the probabilities
   float acc[DPL];
 #pragma unroll
   for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
   const float* vbase = vcache + hoff + lane;
   constexpr int UNR = 8;
   int t = wave;
-  for (; t + (UNR - 1) * kBlockWaves < ncache; t += UNR * kBlockWaves) {
+  for (; t + (UNR - 1) * kAttnWaves < ncache; t += UNR * kAttnWaves) {
     float v[UNR][DPL];
 #pragma unroll
     for (int u = 0; u < UNR; ++u)
 #pragma unroll
       for (int j = 0; j < DPL; ++j)
         v[u][j] = lane + j * kWave < head_size
-                      ? vbase[static_cast<size_t>(t + u * kBlockWaves) * kv_dim + j * kWave]
+                      ? vbase[static_cast<size_t>(t + u * kAttnWaves) * kv_dim + j * kWave]
                       : 0.f;
 #pragma unroll
     for (int u = 0; u < UNR; ++u) {
-      const float p = s_p[t + u * kBlockWaves];
+      const float p = s_p[t + u * kAttnWaves];
 #pragma unroll
       for (int j = 0; j < DPL; ++j) acc[j] = fmaf(p, v[u][j], acc[j]);
     }
   }
-  for (; t < ncache; t += kBlockWaves) {
+  for (; t < ncache; t += kAttnWaves) {
     const float p = s_p[t];
 #pragma unroll
     for (int j = 0; j < DPL; ++j)
       if (lane + j * kWave < head_size)
         acc[j] = fmaf(p, vbase[static_cast<size_t>(t) * kv_dim + j * kWave], acc[j]);
   }
-  if (ROPE && wave == pos % kBlockWaves) {  // position pos from registers, in its wave's order
+  if (ROPE && wave == pos % kAttnWaves) {  // position pos from registers, in its wave's order
     const float p = s_p[pos];
 #pragma unroll
     for (int j = 0; j < DPL; ++j)
@@ -285,10 +290,10 @@ __global__ __launch_bounds__(kBlock) void attention_decode_kernel(
 #pragma unroll
   for (int j = 0; j < DPL; ++j) s_part[wave][lane + j * kWave] = acc[j];
   __syncthreads();
-  for (int d = threadIdx.x; d < head_size; d += kBlock) {
+  for (int d = threadIdx.x; d < head_size; d += kAttnBlock) {
     float o = s_part[0][d];
 #pragma unroll
-    for (int w = 1; w < kBlockWaves; ++w) o += s_part[w][d];
+    for (int w = 1; w < kAttnWaves; ++w) o += s_part[w][d];
     out[head * head_size + d] = o / l;
   }
 }
@@ -495,8 +500,8 @@ int sq8_attention_decode(const float* q, const float* key_cache, const float* va
       head_size > 256 || max_seq <= 0)
     return SQ8_ERR_DIMS;
   const size_t lds = static_cast<size_t>(max_seq) * sizeof(float);
-  if (lds > 64 * 1024) return SQ8_ERR_DIMS;  // scores of one head live in LDS
-  hipLaunchKernelGGL((attention_decode_kernel<256, false>), dim3(head_num), dim3(kBlock), lds,
+  if (lds > 40 * 1024) return SQ8_ERR_DIMS;  // scores of one head live in LDS (<= 10240 positions)
+  hipLaunchKernelGGL((attention_decode_kernel<256, false>), dim3(head_num), dim3(kAttnBlock), lds,
                      stream_of(hip_stream), q, key_cache, value_cache, pos, out, head_num,
                      kv_head_num, head_size, RopeArgs{});
   return launched();
@@ -512,10 +517,10 @@ int sq8_rope_attention_decode(const float* qkv, int head_num, int kv_head_num, i
       head_size % 2 || head_size > 256 || max_seq <= 0)
     return SQ8_ERR_DIMS;
   const size_t lds = static_cast<size_t>(max_seq) * sizeof(float);
-  if (lds > 64 * 1024) return SQ8_ERR_DIMS;
+  if (lds > 40 * 1024) return SQ8_ERR_DIMS;
   const RopeArgs ra{head_num * head_size, kv_head_num * head_size, sin_cache, cos_cache, key_cache,
                     value_cache};
-  hipLaunchKernelGGL((attention_decode_kernel<256, true>), dim3(head_num), dim3(kBlock), lds,
+  hipLaunchKernelGGL((attention_decode_kernel<256, true>), dim3(head_num), dim3(kAttnBlock), lds,
                      stream_of(hip_stream), qkv, key_cache, value_cache, pos, out, head_num,
                      kv_head_num, head_size, ra);
   return launched();
