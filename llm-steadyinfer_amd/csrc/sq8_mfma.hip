@@ -107,9 +107,8 @@ struct Tile {
 
 template <int WAVES_M, int WAVES_N, int TM, int TN>
 __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
-    const _Float16* __restrict__ xh, const _Float16* __restrict__ xl,
-    const float* __restrict__ rscale, const int8_t* __restrict__ w, const float* __restrict__ s,
-    float* __restrict__ out, int M, int N, int K, int gs, int groups_per_split) {
+    const _Float16* xh, const _Float16* xl, const float* __restrict__ rscale, const int8_t* w,
+    const float* s, float* __restrict__ out, int M, int N, int K, int gs, int groups_per_split) {
   using T = Tile<WAVES_M, WAVES_N, TM, TN>;
   extern __shared__ _Float16 lds[];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
@@ -205,10 +204,16 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
     for (int j = 0; j < TN; ++j) cur_s[j] = rs[j];
   }
   __syncthreads();
+  // Branch-free steps: the prefetch and the store of the next stage are unconditional (past the
+  // end they repeat the last step into the stage that is not read again). A load issued on only
+  // one branch makes the compiler's wait counts assume the other branch, so the first use of this
+  // step's data would also wait for the whole prefetch.
   for (int st = st_begin; st < st_end; ++st) {
     const int buf = (st - st_begin) & 1;
-    const bool more = st + 1 < st_end;
-    if (more) gload(st + 1);
+    asm volatile("" ::: "memory");
+    gload(min(st + 1, st_end - 1));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
     const _Float16* sxh = lds + buf * T::STAGE_HALVES;
     const _Float16* sxl = sxh + T::BM * LDS_STRIDE;
     const _Float16* sw = sxl + T::BM * LDS_STRIDE;
@@ -247,11 +252,12 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(cur_s[j], p[i][j][r], acc[i][j][r]);
-    if (more) {
-      lstore(buf ^ 1);
+    // Keep the next stage's conversion after the MFMAs: hoisted into them it would wait for the
+    // prefetch at the top of the step.
+    __builtin_amdgcn_sched_barrier(0);
+    lstore(buf ^ 1);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) cur_s[j] = rs[j];
-    }
+    for (int j = 0; j < TN; ++j) cur_s[j] = rs[j];
     __syncthreads();
   }
 
@@ -726,6 +732,266 @@ __global__ __launch_bounds__(kThreads) void skinny_i8_kernel(
     __hip_atomic_store(&tickets[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---------------------------------------------------------------- small-batch decode tile kernel
+// For 5 <= M <= 64 token rows. Two launches:
+//  * pack_x_kernel splits each token row into f16 hi/lo halves with one power of two per row (the
+//    same split as split_x_kernel) and writes them in MFMA fragment order, so that a wave fetches
+//    the A operand of one 64-wide group for 16 rows with four fully coalesced dwordx4 loads:
+//        xp[g][rt][u][lane] (16 bytes each), u = 2*t + (0 hi | 1 lo), t = K half-step,
+//        lane l holds row 16*rt + l%16, k = 64*g + (l/16)*16 + 8*t .. +8.
+//    Rows M .. 16*RT-1 are written as zeros.
+//  * tile_kernel: a workgroup of W waves owns 16*T output columns and a range of K groups; wave w
+//    takes groups w, w + W, w + 2W, ... of that range, so the W waves of a workgroup together
+//    stream the weight tile front to back. Per group a lane loads, for each of its T column tiles,
+//    the 16 contiguous weight bytes (l/16)*16 .. of row n0 + 16j + l%16 straight into B registers,
+//    plus the tile's scale and the RT*4 A fragments; the next group's loads are issued before the
+//    current group is multiplied (register double buffer). No barrier until the end: the W
+//    per-wave accumulators are summed in LDS in wave order (deterministic), multiplied by the
+//    row's 2^-e and written (or, with K split over gridDim.y, passed through the split-K tickets
+//    as in the skinny kernels).
+// Per group and column tile: P = sum of the hi and lo MFMAs over both half-steps (from zero),
+// acc += scale[n, g] * P. Result lane l: column l%16, rows 16*rt + 4*(l/16) .. +3.
+__global__ __launch_bounds__(kThreads) void pack_x_kernel(const float* __restrict__ x,
+                                                         uint2* __restrict__ xp,
+                                                         float* __restrict__ rscale, int M, int K,
+                                                         int RT) {
+  __shared__ float red[kThreads / kWave];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const int rt = m >> 4;
+  const bool live = m < M;
+  const float* xr = x + static_cast<size_t>(min(m, M - 1)) * K;
+  float amax = 0.f;
+  if (live)
+    for (int k = tid * 4; k < K; k += kThreads * 4) {
+      const float4 v = *reinterpret_cast<const float4*>(xr + k);
+      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+#pragma unroll
+  for (int off = 32; off >= 1; off /= 2) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+  if ((tid & (kWave - 1)) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = 0;
+  if (amax > 0.f && amax <= 3.402823466e38f) {
+    int ex;
+    frexpf(amax, &ex);  // amax = f * 2^ex, f in [0.5, 1)
+    e = min(max(14 - ex, -126), 126);
+  }
+  if (live && tid == 0) rscale[m] = ldexpf(1.f, -e);
+  for (int k = tid * 4; k < K; k += kThreads * 4) {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) v = *reinterpret_cast<const float4*>(xr + k);
+    const float a[4] = {ldexpf(v.x, e), ldexpf(v.y, e), ldexpf(v.z, e), ldexpf(v.w, e)};
+    _Float16 h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      h[i] = static_cast<_Float16>(a[i]);
+      l[i] = static_cast<_Float16>(a[i] - static_cast<float>(h[i]));
+    }
+    const int g = k >> 6, kk = k & 63, t = (kk >> 3) & 1, half = (kk >> 2) & 1;
+    const int lane = (kk >> 4) * 16 + (m & 15);
+    // uint2 index: 16-byte fragment (g, rt, u, lane) holds two uint2; `half` picks one.
+    const size_t frag = ((static_cast<size_t>(g) * RT + rt) * 4 + 2 * t) * kWave + lane;
+    xp[frag * 2 + half] = *reinterpret_cast<const uint2*>(h);
+    xp[(frag + kWave) * 2 + half] = *reinterpret_cast<const uint2*>(l);
+  }
+}
+
+template <int RT, int T, int W, int DEPTH, int GP>
+__global__ __launch_bounds__(W * kWave) void tile_kernel(
+    const u32x4* xp, const float* __restrict__ rscale, const int8_t* w, const float* s,
+    float* __restrict__ y, float* __restrict__ part,
+    unsigned* __restrict__ tickets, int M, int N, int K, int gs, int gps, int splits) {
+  static_assert(W * RT * T <= 64, "LDS reduction buffer above 64 KiB");
+  constexpr int OUTS = RT * T * 4 * kWave;  // accumulator floats per wave
+  constexpr int NT = W * kWave;
+  __shared__ float red[W > 1 ? W * OUTS : 1];
+  __shared__ int is_last;
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lcol = lane & 15, kq = (lane >> 4) * 16;
+  const int n0 = blockIdx.x * (16 * T);
+  const int G = K / BK, gpr = K / gs;
+  // A step is GP consecutive groups, so each 128-byte line of a weight row is read by one wave
+  // in back-to-back loads; wave w takes steps w, w + W, ... of the workgroup's range.
+  const int sbeg = (blockIdx.y * gps) / GP + wave;
+  const int send = min(G, (blockIdx.y + 1) * gps) / GP;
+  const int nst = sbeg < send ? (send - sbeg + W - 1) / W : 0;
+
+  const int8_t* wrow[T];
+  const float* srow[T];
+#pragma unroll
+  for (int j = 0; j < T; ++j) {
+    const int ncol = min(n0 + 16 * j + lcol, N - 1);
+    wrow[j] = w + static_cast<size_t>(ncol) * K + kq;
+    srow[j] = s + static_cast<size_t>(ncol) * gpr;
+  }
+  const u32x4* xlane = xp + lane;
+
+  u32x4 bq[DEPTH][GP][T];
+  float sc[DEPTH][GP][T];
+  bool live_b[DEPTH];
+  u32x4 af[DEPTH][GP][RT][4];
+  // Step i >= nst (the padding up to a multiple of DEPTH) re-reads the last step with scale 0.
+  auto load = [&](int b, int i) __attribute__((always_inline)) {
+    const int g0 = (sbeg + min(i, nst - 1) * W) * GP;
+#pragma unroll
+    for (int h = 0; h < GP; ++h)
+#pragma unroll
+      for (int j = 0; j < T; ++j)
+        bq[b][h][j] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(wrow[j] + static_cast<size_t>(g0 + h) * BK));
+#pragma unroll
+    for (int h = 0; h < GP; ++h) {
+#pragma unroll
+      for (int j = 0; j < T; ++j) sc[b][h][j] = srow[j][((g0 + h) * BK) / gs];
+#pragma unroll
+      for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          af[b][h][r][u] = xlane[((static_cast<size_t>(g0 + h) * RT + r) * 4 + u) * kWave];
+    }
+    live_b[b] = i < nst;  // applied at use: a select here would wait for the scale load
+  };
+
+  f4v acc[RT][T];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int j = 0; j < T; ++j) acc[r][j] = f4v{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int h = 0; h < GP; ++h) {
+      h8 bw[T][2];
+#pragma unroll
+      for (int j = 0; j < T; ++j) {
+        uint32_t hq[8];
+        i8x4_to_h4(bq[b][h][j].x, hq[0], hq[1]);
+        i8x4_to_h4(bq[b][h][j].y, hq[2], hq[3]);
+        i8x4_to_h4(bq[b][h][j].z, hq[4], hq[5]);
+        i8x4_to_h4(bq[b][h][j].w, hq[6], hq[7]);
+        const u32x4 b0 = {hq[0], hq[1], hq[2], hq[3]};
+        const u32x4 b1 = {hq[4], hq[5], hq[6], hq[7]};
+        bw[j][0] = __builtin_bit_cast(h8, b0);
+        bw[j][1] = __builtin_bit_cast(h8, b1);
+      }
+#pragma unroll
+      for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int j = 0; j < T; ++j) {
+          const f4v zero = {0.f, 0.f, 0.f, 0.f};
+          f4v p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, af[b][h][r][0]),
+                                                         bw[j][0], zero, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, af[b][h][r][1]),
+                                                     bw[j][0], p, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, af[b][h][r][2]),
+                                                     bw[j][1], p, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, af[b][h][r][3]),
+                                                     bw[j][1], p, 0, 0, 0);
+          const float scale = live_b[b] ? sc[b][h][j] : 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[r][j][i] = fmaf(scale, p[i], acc[r][j][i]);
+        }
+    }
+  };
+
+  // Ring of DEPTH register buffers: step i lives in buffer i % DEPTH and is loaded DEPTH - 1
+  // steps ahead of its use. Branch-free steady state: nst is padded to a multiple of DEPTH and
+  // every load is issued unconditionally. A load issued on only one branch makes the compiler's
+  // wait counts assume the other branch, and the wait for this step's data would then also wait
+  // for most of the prefetch. The streamed pointers are not __restrict__, so the compiler
+  // barriers pin the loads to their step.
+  if (nst > 0) {
+#pragma unroll
+    for (int d = 0; d < DEPTH - 1; ++d) load(d, d);
+    for (int i = 0; i < nst; i += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        asm volatile("" ::: "memory");
+        load((d + DEPTH - 1) % DEPTH, i + d + DEPTH - 1);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        compute(d);
+      }
+    }
+  }
+
+  // Sum the W waves' accumulators in wave order; output o = ((r*T + j)*4 + i)*64 + lane.
+  float out[(OUTS + NT - 1) / NT];
+  if constexpr (W > 1) {
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int j = 0; j < T; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave * OUTS + ((r * T + j) * 4 + i) * kWave + lane] = acc[r][j][i];
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < (OUTS + NT - 1) / NT; ++q) {
+      const int o = tid + q * NT;
+      float v = 0.f;
+      if (o < OUTS)
+        for (int z = 0; z < W; ++z) v += red[z * OUTS + o];
+      out[q] = v;
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int j = 0; j < T; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) out[(r * T + j) * 4 + i] = acc[r][j][i];
+  }
+  auto coords = [&](int q, int& m, int& n) __attribute__((always_inline)) {
+    const int o = W > 1 ? tid + q * NT : q * kWave + lane;
+    const int ln = o & (kWave - 1), ri = o / kWave;  // ri = (r*T + j)*4 + i
+    const int i = ri & 3, j = (ri >> 2) % T, r = (ri >> 2) / T;
+    m = 16 * r + 4 * (ln >> 4) + i;
+    n = n0 + 16 * j + (ln & 15);
+    return o < OUTS;
+  };
+  constexpr int NQ = (OUTS + NT - 1) / NT;
+  if (splits == 1) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      int m, n;
+      if (coords(q, m, n) && m < M && n < N)
+        y[static_cast<size_t>(m) * N + n] = out[q] * rscale[m];
+    }
+    return;
+  }
+  float* dst = part + static_cast<size_t>(blockIdx.y) * M * N;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    int m, n;
+    if (coords(q, m, n) && m < M && n < N)
+      __hip_atomic_store(dst + static_cast<size_t>(m) * N + n, out[q] * rscale[m],
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // Wait until this thread's partial stores are acknowledged before the workgroup takes its
+  // ticket; the last workgroup of the column block sums the splits in order.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0)
+    is_last = __hip_atomic_fetch_add(&tickets[blockIdx.x], 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) == static_cast<unsigned>(splits - 1);
+  __syncthreads();
+  if (!is_last) return;
+  const int ncols = min(16 * T, N - n0);
+  for (int idx = tid; idx < M * ncols; idx += NT) {
+    const int m = idx / ncols, nn = n0 + idx % ncols;
+    const size_t o = static_cast<size_t>(m) * N + nn;
+    float v = __hip_atomic_load(part + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int z = 1; z < splits; ++z)
+      v += __hip_atomic_load(part + static_cast<size_t>(z) * M * N + o, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    y[o] = v;
+  }
+  if (tid == 0)
+    __hip_atomic_store(&tickets[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Sum split-K partials in split order: y[i] = sum_z part[z][i].
 __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(const float* __restrict__ part,
                                                                 float* __restrict__ y,
@@ -744,6 +1010,8 @@ size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 constexpr int kSkinnyMaxM = 32;
 
 struct Plan {
+  bool tile;      // pack_x_kernel + tile_kernel (9 <= M <= 64)
+  int rt, tn, tw; // tile: 16-row activation tiles, 16-column tiles per wave, waves per workgroup
   bool skinny;
   int kw;         // skinny: K groups per chunk (divides groups_per_split)
   int cfg;        // GEMM: 0: 32x256 tile, 1: 64x128, 2: 128x128.  Skinny: 0: MT=1, 1: MT=2
@@ -756,6 +1024,30 @@ Plan make_plan(int M, int N, int K) {
   Plan p{};
   const int nsteps = K / BK;
   const int target = 2 * cu_count();
+  const int rt = (M + 15) / 16;
+  // Tile kernel for 9..64 tokens, except long rows (K >= 8192) at 16 or fewer tokens (the skinny
+  // kernel is faster there) and at more than 32 tokens (the GEMM is). Configurations from MI355X
+  // sweeps over the Llama-3-8B projections: wide outputs (N >= 16384) take 4 column tiles per
+  // wave and no K split; others take 2 tiles, 8 waves, and split K when the grid has at most
+  // 1024 waves.
+  if (M > 8 && M <= 64 && !(K >= 8192 && (rt == 1 || rt > 2))) {
+    p.tile = true;
+    p.rt = rt;
+    int splits = 1;
+    if (N >= 16384) {
+      p.tn = 4;
+      p.tw = rt <= 2 ? 4 : 2;
+    } else {
+      p.tn = 2;
+      p.tw = 8;
+      const int waves = ((N + 31) / 32) * p.tw;
+      const int smax = std::max(1, nsteps / p.tw);  // at least one group per wave
+      if (waves <= 1024) splits = std::min(smax, (2048 + waves - 1) / waves);
+    }
+    p.groups_per_split = (nsteps + splits - 1) / splits;
+    p.splits = (nsteps + p.groups_per_split - 1) / p.groups_per_split;
+    return p;
+  }
   if (M <= kSkinnyMaxM) {
     p.skinny = true;
     p.cfg = 0;
@@ -826,6 +1118,27 @@ hipError_t launch_skinny_i8(const float* x, const int8_t* w, const float* s, flo
   return hipGetLastError();
 }
 
+template <int RT, int T, int W>
+hipError_t launch_tile(const float* x, const int8_t* w, const float* s, float* y, void* ws, int M,
+                       int N, int K, int gs, const Plan& p, hipStream_t st) {
+  static_assert(W * RT * T <= 64, "tile_kernel LDS reduction buffer");
+  unsigned* tickets = static_cast<unsigned*>(ws);
+  char* base = static_cast<char*>(ws) + kTicketBytes;
+  u32x4* xp = reinterpret_cast<u32x4*>(base);
+  base += align256(static_cast<size_t>(K / BK) * RT * 4 * kWave * sizeof(u32x4));
+  float* rsc = reinterpret_cast<float*>(base);
+  base += align256(static_cast<size_t>(16 * RT) * sizeof(float));
+  float* part = reinterpret_cast<float*>(base);
+  hipLaunchKernelGGL(pack_x_kernel, dim3(16 * RT), dim3(kThreads), 0, st, x,
+                     reinterpret_cast<uint2*>(xp), rsc, M, K, RT);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const dim3 grid((N + 16 * T - 1) / (16 * T), p.splits);
+  hipLaunchKernelGGL((tile_kernel<RT, T, W, 2, 1>), grid, dim3(W * kWave), 0, st, xp, rsc, w, s,
+                     y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 // Workspace layout: [ticket array, kTicketBytes][path buffers]. The ticket array must be zero
@@ -833,7 +1146,10 @@ hipError_t launch_skinny_i8(const float* x, const int8_t* w, const float* s, flo
 size_t mfma_workspace_bytes(int M, int N, int K) {
   const Plan p = make_plan(M, N, K);
   size_t b = kTicketBytes;
-  if (!p.skinny) {
+  if (p.tile) {
+    b += align256(static_cast<size_t>(K / BK) * p.rt * 4 * kWave * sizeof(u32x4));
+    b += align256(static_cast<size_t>(16 * p.rt) * sizeof(float));
+  } else if (!p.skinny) {
     b += 2 * align256(static_cast<size_t>(M) * K * sizeof(_Float16));
     b += align256(static_cast<size_t>(M) * sizeof(float));
   }
@@ -848,6 +1164,20 @@ hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y
   const Plan p = make_plan(M, N, K);
   unsigned* tickets = static_cast<unsigned*>(ws);
   char* base = static_cast<char*>(ws) + kTicketBytes;
+  if (p.tile) {
+    const int key = p.rt * 100 + p.tn * 10 + (p.tw >= 8 ? 8 : p.tw);
+    switch (key) {
+      case 128: return launch_tile<1, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st);
+      case 144: return launch_tile<1, 4, 4>(x, w, s, y, ws, M, N, K, gs, p, st);
+      case 228: return launch_tile<2, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st);
+      case 244: return launch_tile<2, 4, 4>(x, w, s, y, ws, M, N, K, gs, p, st);
+      case 328: return launch_tile<3, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st);
+      case 342: return launch_tile<3, 4, 2>(x, w, s, y, ws, M, N, K, gs, p, st);
+      case 428: return launch_tile<4, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st);
+      case 442: return launch_tile<4, 4, 2>(x, w, s, y, ws, M, N, K, gs, p, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
   if (p.skinny) {
     float* part = reinterpret_cast<float*>(base);
 #define SQ8_SKINNY(MR, MT16)                                                               \

@@ -98,7 +98,7 @@ def _row_subset(N, count, seed):
     return rows
 
 
-@pytest.mark.parametrize("M", [1, 8, 32, 64, 2048])
+@pytest.mark.parametrize("M", [1, 8, 16, 32, 48, 64, 2048])
 @pytest.mark.parametrize("proj", list(LLAMA3_8B))
 def test_llama3_8b_shapes(sq8, dev, proj, M):
     """Full BASELINE shapes on the GPU; the oracle checks a subset of output rows (rows are
