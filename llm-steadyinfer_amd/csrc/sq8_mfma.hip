@@ -281,6 +281,8 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
 
 // Split-K tickets live at the start of the workspace; each call leaves them zero.
 constexpr int kTicketBytes = 64 * 1024;  // ticket array at the start of the workspace
+// K groups per split of the tile kernel: bounds its LDS scale stage (16*T rows x this many).
+constexpr int kTileScaleGroups = 128;
 
 // ---------------------------------------------------------------- skinny decode kernel
 // For 3 <= M <= 64 token rows: one launch, no activation prologue, v_mfma_f32_16x16x32_f16 on
@@ -797,15 +799,19 @@ __global__ __launch_bounds__(kThreads) void pack_x_kernel(const float* __restric
   }
 }
 
-template <int RT, int T, int W, int DEPTH, int GP>
+template <int RT, int T, int W>
 __global__ __launch_bounds__(W * kWave) void tile_kernel(
     const u32x4* xp, const float* __restrict__ rscale, const int8_t* w, const float* s,
     float* __restrict__ y, float* __restrict__ part,
     unsigned* __restrict__ tickets, int M, int N, int K, int gs, int gps, int splits) {
-  static_assert(W * RT * T <= 64, "LDS reduction buffer above 64 KiB");
   constexpr int OUTS = RT * T * 4 * kWave;  // accumulator floats per wave
   constexpr int NT = W * kWave;
-  __shared__ float red[W > 1 ? W * OUTS : 1];
+  constexpr int SROWS = 16 * T;             // weight rows (output columns) of the workgroup
+  constexpr int LDSF = (W > 1 ? W * OUTS : 0) > SROWS * kTileScaleGroups
+                           ? W * OUTS : SROWS * kTileScaleGroups;
+  static_assert(LDSF * 4 <= 64 * 1024, "tile_kernel LDS above 64 KiB");
+  // Scale stage [SROWS][gps] during the main loop, then the cross-wave reduction buffer.
+  __shared__ float lds[LDSF];
   __shared__ int is_last;
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
@@ -813,46 +819,45 @@ __global__ __launch_bounds__(W * kWave) void tile_kernel(
   const int lcol = lane & 15, kq = (lane >> 4) * 16;
   const int n0 = blockIdx.x * (16 * T);
   const int G = K / BK, gpr = K / gs;
-  // A step is GP consecutive groups, so each 128-byte line of a weight row is read by one wave
-  // in back-to-back loads; wave w takes steps w, w + W, ... of the workgroup's range.
-  const int sbeg = (blockIdx.y * gps) / GP + wave;
-  const int send = min(G, (blockIdx.y + 1) * gps) / GP;
-  const int nst = sbeg < send ? (send - sbeg + W - 1) / W : 0;
+  const int gsplit = blockIdx.y * gps;              // first group of this split
+  const int gcount = min(G, gsplit + gps) - gsplit; // groups in this split (<= kTileScaleGroups)
+  const int nst = wave < gcount ? (gcount - wave + W - 1) / W : 0;
+
+  // Stage the split's scales of the workgroup's rows in LDS: row-contiguous, coalesced loads.
+  // Per-lane loads in the MFMA layout would touch 16 rows per instruction, once per group.
+  for (int idx = tid; idx < SROWS * gcount; idx += NT) {
+    const int r = idx / gcount, gi = idx - r * gcount;
+    const int n = min(n0 + r, N - 1);
+    lds[r * gcount + gi] = s[static_cast<size_t>(n) * gpr + ((gsplit + gi) * BK) / gs];
+  }
 
   const int8_t* wrow[T];
-  const float* srow[T];
 #pragma unroll
-  for (int j = 0; j < T; ++j) {
-    const int ncol = min(n0 + 16 * j + lcol, N - 1);
-    wrow[j] = w + static_cast<size_t>(ncol) * K + kq;
-    srow[j] = s + static_cast<size_t>(ncol) * gpr;
-  }
+  for (int j = 0; j < T; ++j)
+    wrow[j] = w + static_cast<size_t>(min(n0 + 16 * j + lcol, N - 1)) * K + kq;
   const u32x4* xlane = xp + lane;
 
-  u32x4 bq[DEPTH][GP][T];
-  float sc[DEPTH][GP][T];
-  bool live_b[DEPTH];
-  u32x4 af[DEPTH][GP][RT][4];
-  // Step i >= nst (the padding up to a multiple of DEPTH) re-reads the last step with scale 0.
+  // Wave w takes groups w, w + W, ... of the split: the W waves of a workgroup read neighbouring
+  // 64-byte pieces of the same rows at about the same time, which streams best from HBM.
+  u32x4 bq[2][T];
+  u32x4 af[2][RT][4];
+  bool live_b[2];
+  int gi_b[2];
+  // Step i >= nst (the padding to an even count) re-reads the last group with scale 0.
   auto load = [&](int b, int i) __attribute__((always_inline)) {
-    const int g0 = (sbeg + min(i, nst - 1) * W) * GP;
+    const int gi = wave + min(i, nst - 1) * W;
+    const int g = gsplit + gi;
 #pragma unroll
-    for (int h = 0; h < GP; ++h)
+    for (int j = 0; j < T; ++j)
+      bq[b][j] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(wrow[j] + static_cast<size_t>(g) * BK));
 #pragma unroll
-      for (int j = 0; j < T; ++j)
-        bq[b][h][j] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(wrow[j] + static_cast<size_t>(g0 + h) * BK));
+    for (int r = 0; r < RT; ++r)
 #pragma unroll
-    for (int h = 0; h < GP; ++h) {
-#pragma unroll
-      for (int j = 0; j < T; ++j) sc[b][h][j] = srow[j][((g0 + h) * BK) / gs];
-#pragma unroll
-      for (int r = 0; r < RT; ++r)
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-          af[b][h][r][u] = xlane[((static_cast<size_t>(g0 + h) * RT + r) * 4 + u) * kWave];
-    }
-    live_b[b] = i < nst;  // applied at use: a select here would wait for the scale load
+      for (int u = 0; u < 4; ++u)
+        af[b][r][u] = xlane[((static_cast<size_t>(g) * RT + r) * 4 + u) * kWave];
+    live_b[b] = i < nst;
+    gi_b[b] = gi;
   };
 
   f4v acc[RT][T];
@@ -861,65 +866,66 @@ __global__ __launch_bounds__(W * kWave) void tile_kernel(
 #pragma unroll
     for (int j = 0; j < T; ++j) acc[r][j] = f4v{0.f, 0.f, 0.f, 0.f};
   auto compute = [&](int b) __attribute__((always_inline)) {
+    h8 bw[T][2];
+    float sc[T];
 #pragma unroll
-    for (int h = 0; h < GP; ++h) {
-      h8 bw[T][2];
+    for (int j = 0; j < T; ++j) {
+      uint32_t hq[8];
+      i8x4_to_h4(bq[b][j].x, hq[0], hq[1]);
+      i8x4_to_h4(bq[b][j].y, hq[2], hq[3]);
+      i8x4_to_h4(bq[b][j].z, hq[4], hq[5]);
+      i8x4_to_h4(bq[b][j].w, hq[6], hq[7]);
+      const u32x4 b0 = {hq[0], hq[1], hq[2], hq[3]};
+      const u32x4 b1 = {hq[4], hq[5], hq[6], hq[7]};
+      bw[j][0] = __builtin_bit_cast(h8, b0);
+      bw[j][1] = __builtin_bit_cast(h8, b1);
+      const float v = lds[(16 * j + lcol) * gcount + gi_b[b]];
+      sc[j] = live_b[b] ? v : 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
 #pragma unroll
       for (int j = 0; j < T; ++j) {
-        uint32_t hq[8];
-        i8x4_to_h4(bq[b][h][j].x, hq[0], hq[1]);
-        i8x4_to_h4(bq[b][h][j].y, hq[2], hq[3]);
-        i8x4_to_h4(bq[b][h][j].z, hq[4], hq[5]);
-        i8x4_to_h4(bq[b][h][j].w, hq[6], hq[7]);
-        const u32x4 b0 = {hq[0], hq[1], hq[2], hq[3]};
-        const u32x4 b1 = {hq[4], hq[5], hq[6], hq[7]};
-        bw[j][0] = __builtin_bit_cast(h8, b0);
-        bw[j][1] = __builtin_bit_cast(h8, b1);
+        const f4v zero = {0.f, 0.f, 0.f, 0.f};
+        f4v p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, af[b][r][0]),
+                                                       bw[j][0], zero, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, af[b][r][1]), bw[j][0],
+                                                   p, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, af[b][r][2]), bw[j][1],
+                                                   p, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, af[b][r][3]), bw[j][1],
+                                                   p, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[r][j][i] = fmaf(sc[j], p[i], acc[r][j][i]);
       }
-#pragma unroll
-      for (int r = 0; r < RT; ++r)
-#pragma unroll
-        for (int j = 0; j < T; ++j) {
-          const f4v zero = {0.f, 0.f, 0.f, 0.f};
-          f4v p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, af[b][h][r][0]),
-                                                         bw[j][0], zero, 0, 0, 0);
-          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, af[b][h][r][1]),
-                                                     bw[j][0], p, 0, 0, 0);
-          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, af[b][h][r][2]),
-                                                     bw[j][1], p, 0, 0, 0);
-          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, af[b][h][r][3]),
-                                                     bw[j][1], p, 0, 0, 0);
-          const float scale = live_b[b] ? sc[b][h][j] : 0.f;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[r][j][i] = fmaf(scale, p[i], acc[r][j][i]);
-        }
-    }
   };
 
-  // Ring of DEPTH register buffers: step i lives in buffer i % DEPTH and is loaded DEPTH - 1
-  // steps ahead of its use. Branch-free steady state: nst is padded to a multiple of DEPTH and
-  // every load is issued unconditionally. A load issued on only one branch makes the compiler's
-  // wait counts assume the other branch, and the wait for this step's data would then also wait
-  // for most of the prefetch. The streamed pointers are not __restrict__, so the compiler
-  // barriers pin the loads to their step.
-  if (nst > 0) {
-#pragma unroll
-    for (int d = 0; d < DEPTH - 1; ++d) load(d, d);
-    for (int i = 0; i < nst; i += DEPTH) {
-#pragma unroll
-      for (int d = 0; d < DEPTH; ++d) {
-        asm volatile("" ::: "memory");
-        load((d + DEPTH - 1) % DEPTH, i + d + DEPTH - 1);
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_sched_barrier(0);
-        compute(d);
-      }
-    }
+  // Register double buffer, branch-free: the step count is padded to even and every load is
+  // issued unconditionally. A load issued on only one branch makes the compiler's wait counts
+  // assume the other branch, and the wait for this step's data would then also wait for most of
+  // the prefetch. The streamed pointers are not __restrict__, so the compiler barriers pin the
+  // loads to their step. The scale stage was written before the first weight loads, so the
+  // barrier's wait for it does not wait for them.
+  if (nst > 0) load(0, 0);
+  __syncthreads();
+  for (int i = 0; i < nst; i += 2) {
+    asm volatile("" ::: "memory");
+    load(1, i + 1);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    compute(0);
+    asm volatile("" ::: "memory");
+    load(0, i + 2);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    compute(1);
   }
+  __syncthreads();  // the scale stage is reused below
 
   // Sum the W waves' accumulators in wave order; output o = ((r*T + j)*4 + i)*64 + lane.
   float out[(OUTS + NT - 1) / NT];
   if constexpr (W > 1) {
+    float* red = lds;
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
@@ -932,7 +938,7 @@ __global__ __launch_bounds__(W * kWave) void tile_kernel(
       const int o = tid + q * NT;
       float v = 0.f;
       if (o < OUTS)
-        for (int z = 0; z < W; ++z) v += red[z * OUTS + o];
+        for (int z = 0; z < W; ++z) v += lds[z * OUTS + o];
       out[q] = v;
     }
   } else {
@@ -1044,6 +1050,7 @@ Plan make_plan(int M, int N, int K) {
       const int smax = std::max(1, nsteps / p.tw);  // at least one group per wave
       if (waves <= 1024) splits = std::min(smax, (2048 + waves - 1) / waves);
     }
+    splits = std::max(splits, (nsteps + kTileScaleGroups - 1) / kTileScaleGroups);
     p.groups_per_split = (nsteps + splits - 1) / splits;
     p.splits = (nsteps + p.groups_per_split - 1) / p.groups_per_split;
     return p;
@@ -1121,7 +1128,6 @@ hipError_t launch_skinny_i8(const float* x, const int8_t* w, const float* s, flo
 template <int RT, int T, int W>
 hipError_t launch_tile(const float* x, const int8_t* w, const float* s, float* y, void* ws, int M,
                        int N, int K, int gs, const Plan& p, hipStream_t st) {
-  static_assert(W * RT * T <= 64, "tile_kernel LDS reduction buffer");
   unsigned* tickets = static_cast<unsigned*>(ws);
   char* base = static_cast<char*>(ws) + kTicketBytes;
   u32x4* xp = reinterpret_cast<u32x4*>(base);
@@ -1134,7 +1140,7 @@ hipError_t launch_tile(const float* x, const int8_t* w, const float* s, float* y
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const dim3 grid((N + 16 * T - 1) / (16 * T), p.splits);
-  hipLaunchKernelGGL((tile_kernel<RT, T, W, 2, 1>), grid, dim3(W * kWave), 0, st, xp, rsc, w, s,
+  hipLaunchKernelGGL((tile_kernel<RT, T, W>), grid, dim3(W * kWave), 0, st, xp, rsc, w, s,
                      y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits);
   return hipGetLastError();
 }
