@@ -303,10 +303,9 @@ constexpr int kTileScaleGroups = 128;
 // before the workgroup takes its ticket.
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-template <int MR, int KW, int TN, int MT16>
+template <int MR, int KW, int TN, int MT16, bool F4>
 __global__ __launch_bounds__(kThreads) void skinny16_kernel(
-    const float* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ s,
-    float* __restrict__ y, float* __restrict__ part, unsigned* __restrict__ tickets, int M, int N,
+    const float* x, const int8_t* w, const float* s, float* __restrict__ y, float* __restrict__ part, unsigned* __restrict__ tickets, int M, int N,
     int K, int gs, int gps, int splits) {
   constexpr int BMP = 16 * MT16;                   // MFMA rows: MT16 stacked 16-row tiles
   static_assert(MR <= BMP && (MR == 8 || MR % 16 == 0), "rows loaded per chunk");
@@ -357,8 +356,18 @@ __global__ __launch_bounds__(kThreads) void skinny16_kernel(
       for (int j = 0; j < TN; ++j) {
         wr[b][q][j] = __builtin_nontemporal_load(
             reinterpret_cast<const u32x4*>(wsrc[j] + (c * KW + q) * BK));
-        wsc[b][q][j] = ssrc[j][((gbeg + c * KW + q) * BK) / gs];
+        if constexpr (!F4) wsc[b][q][j] = ssrc[j][((gbeg + c * KW + q) * BK) / gs];
       }
+    if constexpr (F4) {  // group_size 64, KW == 4: the chunk's 4 scales of a row are one float4
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const float4 v = *reinterpret_cast<const float4*>(ssrc[j] + gbeg + c * KW);
+        wsc[b][0][j] = v.x;
+        wsc[b][1][j] = v.y;
+        wsc[b][2][j] = v.z;
+        wsc[b][3][j] = v.w;
+      }
+    }
   };
   float4 xr[XF4];
   auto xload = [&](int c) __attribute__((always_inline)) {
@@ -399,6 +408,7 @@ __global__ __launch_bounds__(kThreads) void skinny16_kernel(
     }
   };
 
+  static_assert(!F4 || KW == 4, "float4 scales cover a 4-group chunk");
   f4v acc[MT16][TN];
 #pragma unroll
   for (int i = 0; i < MT16; ++i)
@@ -448,8 +458,12 @@ __global__ __launch_bounds__(kThreads) void skinny16_kernel(
   };
 
   // Chunk c: weights in wr[c & 1], activations in LDS buffer c & 1. The next chunk's activation
-  // loads are issued before its weight loads (a scheduling barrier keeps that order): vmcnt
-  // retires in issue order, so waiting for the activations leaves the weight prefetch in flight.
+  // loads are issued before its weight loads (compiler and scheduling barriers keep that order):
+  // vmcnt retires in issue order, so waiting for the activations leaves the weight prefetch in
+  // flight. The prefetch and the store of the next buffer are unconditional (past the end they
+  // repeat the last chunk into the buffer that is not read again): a load issued on only one
+  // branch makes the compiler's wait counts assume the other branch, and the wait for this
+  // chunk's data would then also wait for the whole prefetch.
   if (nch > 0) {
     xload(0);
     wload(0, 0);
@@ -458,12 +472,17 @@ __global__ __launch_bounds__(kThreads) void skinny16_kernel(
   __syncthreads();
   auto step = [&](auto buf, int c) __attribute__((always_inline)) {
     constexpr int B = decltype(buf)::value;
-    const bool more = c + 1 < nch;
-    if (more) xload(c + 1);
+    const int cn = min(c + 1, nch - 1);
+    asm volatile("" ::: "memory");
+    xload(cn);
+    asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    if (more) wload(B ^ 1, c + 1);
+    wload(B ^ 1, cn);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
     compute(B);
-    if (more) xstore(B ^ 1);
+    __builtin_amdgcn_sched_barrier(0);
+    xstore(B ^ 1);
     __syncthreads();
   };
   for (int c = 0; c < nch;) {
@@ -1110,8 +1129,15 @@ hipError_t launch_skinny16(const float* x, const int8_t* w, const float* s, floa
                            unsigned* tickets, int M, int N, int K, int gs, const Plan& p,
                            hipStream_t st) {
   const dim3 grid((N + 64 * TN - 1) / (64 * TN), p.splits);
-  hipLaunchKernelGGL((skinny16_kernel<MR, KW, TN, MT16>), grid, dim3(kThreads), 0, st, x, w, s, y, part,
-                     tickets, M, N, K, gs, p.groups_per_split, p.splits);
+  // float4 scale loads need 4-group chunks at 16-byte aligned addresses
+  const bool f4 = KW == 4 && gs == BK && (K / BK) % 4 == 0 &&
+                  (reinterpret_cast<uintptr_t>(s) & 15) == 0;
+  if (f4)
+    hipLaunchKernelGGL((skinny16_kernel<MR, KW, TN, MT16, KW == 4>), grid, dim3(kThreads), 0, st,
+                       x, w, s, y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits);
+  else
+    hipLaunchKernelGGL((skinny16_kernel<MR, KW, TN, MT16, false>), grid, dim3(kThreads), 0, st, x,
+                       w, s, y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits);
   return hipGetLastError();
 }
 
