@@ -560,10 +560,9 @@ __global__ __launch_bounds__(kThreads) void skinny16_kernel(
 typedef int i32x4v __attribute__((ext_vector_type(4)));
 constexpr int kLimbRowBytes = 80;  // 64 limb bytes + 16 padding: conflict-free ds_read_b128
 
-template <int NB, int KW, int TN>
+template <int NB, int KW, int TN, bool F4>
 __global__ __launch_bounds__(kThreads) void skinny_i8_kernel(
-    const float* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ s,
-    float* __restrict__ y, float* __restrict__ part, unsigned* __restrict__ tickets, int M, int N,
+    const float* x, const int8_t* w, const float* s, float* __restrict__ y, float* __restrict__ part, unsigned* __restrict__ tickets, int M, int N,
     int K, int gs, int gps, int splits) {
   constexpr int MT = 4 * NB;                       // token slots
   constexpr int ROWS = 16 * NB;                    // A rows (4 limbs per token)
@@ -601,8 +600,18 @@ __global__ __launch_bounds__(kThreads) void skinny_i8_kernel(
       for (int j = 0; j < TN; ++j) {
         wr[b][q][j] = __builtin_nontemporal_load(
             reinterpret_cast<const i32x4v*>(wsrc[j] + (c * KW + q) * BK));
-        wsc[b][q][j] = ssrc[j][((gbeg + c * KW + q) * BK) / gs];
+        if constexpr (!F4) wsc[b][q][j] = ssrc[j][((gbeg + c * KW + q) * BK) / gs];
       }
+    if constexpr (F4) {  // group_size 64, KW == 4: the chunk's 4 scales of a row are one float4
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const float4 v = *reinterpret_cast<const float4*>(ssrc[j] + gbeg + c * KW);
+        wsc[b][0][j] = v.x;
+        wsc[b][1][j] = v.y;
+        wsc[b][2][j] = v.z;
+        wsc[b][3][j] = v.w;
+      }
+    }
   };
   float4 xr[XPT];
   auto xload = [&](int c) __attribute__((always_inline)) {
@@ -654,6 +663,7 @@ __global__ __launch_bounds__(kThreads) void skinny_i8_kernel(
     }
   };
 
+  static_assert(!F4 || KW == 4, "float4 scales cover a 4-group chunk");
   float acc[NB][TN];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
@@ -694,14 +704,22 @@ __global__ __launch_bounds__(kThreads) void skinny_i8_kernel(
     xstore(0);
   }
   __syncthreads();
+  // Branch-free steps, as in the f16 skinny kernel: the prefetch and the store of the next
+  // buffer are unconditional (past the end they repeat the last chunk into the buffer that is
+  // not read again), so the compiler's wait counts never assume a branch without the prefetch.
   auto step = [&](auto buf, int c) __attribute__((always_inline)) {
     constexpr int B = decltype(buf)::value;
-    const bool more = c + 1 < nch;
-    if (more) xload(c + 1);
+    const int cn = min(c + 1, nch - 1);
+    asm volatile("" ::: "memory");
+    xload(cn);
+    asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    if (more) wload(B ^ 1, c + 1);
+    wload(B ^ 1, cn);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
     compute(B);
-    if (more) xstore(B ^ 1);
+    __builtin_amdgcn_sched_barrier(0);
+    xstore(B ^ 1);
     __syncthreads();
   };
   for (int c = 0; c < nch;) {
@@ -1146,8 +1164,14 @@ hipError_t launch_skinny_i8(const float* x, const int8_t* w, const float* s, flo
                             unsigned* tickets, int M, int N, int K, int gs, const Plan& p,
                             hipStream_t st) {
   const dim3 grid((N + 64 * TN - 1) / (64 * TN), p.splits);
-  hipLaunchKernelGGL((skinny_i8_kernel<NB, KW, TN>), grid, dim3(kThreads), 0, st, x, w, s, y,
-                     part, tickets, M, N, K, gs, p.groups_per_split, p.splits);
+  const bool f4 = KW == 4 && gs == BK && (K / BK) % 4 == 0 &&
+                  (reinterpret_cast<uintptr_t>(s) & 15) == 0;
+  if (f4)
+    hipLaunchKernelGGL((skinny_i8_kernel<NB, KW, TN, KW == 4>), grid, dim3(kThreads), 0, st, x,
+                       w, s, y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits);
+  else
+    hipLaunchKernelGGL((skinny_i8_kernel<NB, KW, TN, false>), grid, dim3(kThreads), 0, st, x, w,
+                       s, y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits);
   return hipGetLastError();
 }
 
