@@ -161,6 +161,48 @@ __global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restri
   extern __shared__ float xs[];
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
+  const int nblk = (N + R - 1) / R;
+  const int GW = gridDim.x * WV;
+  const int gs = GS ? GS : gs_rt;
+  const int gpr = K / gs;
+  const int nsteps = (K + 1024 * U - 1) / (1024 * U);
+  // The scales of a step are loaded one step ahead. Needed only after the dot products, they would
+  // otherwise be scheduled after them and add a second memory round trip to every step. Rows
+  // past N (including those of a block past the last) are clamped to row N - 1.
+  auto load_scales = [&](int b, int st, float (&sc)[U][R]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = (st * U + u) * 1024 + lane * 16;
+      const int kc = !TAIL || k < K ? k : 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        sc[u][r] = s[static_cast<size_t>(min(b * R + r, N - 1)) * gpr + kc / gs];
+    }
+  };
+  auto load_w = [&](int b, int st, i32x4 (&q)[U][R]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = (st * U + u) * 1024 + lane * 16;
+      const bool ok = !TAIL || k < K;
+      const int kc = ok ? k : 0;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int n = min(b * R + r, N - 1);
+        const i32x4 v = __builtin_nontemporal_load(
+            reinterpret_cast<const i32x4*>(w + static_cast<size_t>(n) * K + kc));
+        q[u][r] = ok ? v : i32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  // The first step's weights and scales are requested before the activations are staged, so
+  // their memory latency overlaps the staging (and its barrier) instead of following it. Waves
+  // without a block (the tail of the last workgroup) read row N - 1 and discard it.
+  int b = blockIdx.x * WV + wave, st = 0;
+  i32x4 q[U][R];
+  float scn[U][R];
+  load_w(b, 0, q);
+  load_scales(b, 0, scn);
+
   // Token rows M .. MT-1 are staged as zeros. float4 number i is stored at i ^ ((i >> 4) & 3): a
   // lane reads the 4 float4 of its 16-element chunk, and without the swizzle lanes l and l+4 would
   // hit the same LDS banks in every ds_read_b128 (4-way conflicts).
@@ -209,51 +251,17 @@ __global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restri
     }
   } else {
     for (int i = tid; i < K / 4; i += WV * kWave) {
-      const float4 a = x4[i], b = x4[K / 4 + i];
-      xs4[i ^ ((i >> 4) & 3)] = make_float4(silu_mul(a.x, b.x), silu_mul(a.y, b.y),
-                                            silu_mul(a.z, b.z), silu_mul(a.w, b.w));
+      const float4 a = x4[i], g = x4[K / 4 + i];
+      xs4[i ^ ((i >> 4) & 3)] = make_float4(silu_mul(a.x, g.x), silu_mul(a.y, g.y),
+                                            silu_mul(a.z, g.z), silu_mul(a.w, g.w));
     }
   }
   __syncthreads();
-  const int nblk = (N + R - 1) / R;
-  const int GW = gridDim.x * WV;
-  const int gs = GS ? GS : gs_rt;
-  const int gpr = K / gs;
-  const int nsteps = (K + 1024 * U - 1) / (1024 * U);
-  // The scales of a step are loaded one step ahead. Needed only after the dot products, they would
-  // otherwise be scheduled after them and add a second memory round trip to every step. Rows
-  // past N (including those of a block past the last) are clamped to row N - 1.
-  auto load_scales = [&](int b, int st, float (&sc)[U][R]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = (st * U + u) * 1024 + lane * 16;
-      const int kc = !TAIL || k < K ? k : 0;
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        sc[u][r] = s[static_cast<size_t>(min(b * R + r, N - 1)) * gpr + kc / gs];
-    }
-  };
+
   float acc[R * MT];
 #pragma unroll
   for (int i = 0; i < R * MT; ++i) acc[i] = 0.f;
-  int b = blockIdx.x * WV + wave, st = 0;
-  float scn[U][R];
-  load_scales(b, st, scn);
-  while (b < nblk) {
-    i32x4 q[U][R];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = (st * U + u) * 1024 + lane * 16;
-      const bool ok = !TAIL || k < K;
-      const int kc = ok ? k : 0;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int n = min(b * R + r, N - 1);
-        const i32x4 v = __builtin_nontemporal_load(
-            reinterpret_cast<const i32x4*>(w + static_cast<size_t>(n) * K + kc));
-        q[u][r] = ok ? v : i32x4{0, 0, 0, 0};
-      }
-    }
+  auto step = [&]() __attribute__((always_inline)) {
     float sc[U][R];
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -290,6 +298,11 @@ __global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restri
     }
     b = b1;
     st = st1;
+  };
+  if (b < nblk) step();  // first step: weights already requested
+  while (b < nblk) {
+    load_w(b, st, q);
+    step();
   }
 }
 
