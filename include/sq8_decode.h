@@ -55,8 +55,9 @@ int sq8_rope_kv(float* qkv, int dim, int kv_dim, int head_size, const int32_t* p
 
 /* Causal attention of one query token at position *pos over cache rows 0..*pos:
  * out[h] = softmax_t(q[h] . K[t][g(h)] / sqrt(head_size)) . V[t][g(h)] with the grouped-query
- * head map g(h) = h * kv_head_num / head_num (at most 10240 cache positions; flash_decoding_kernel + combine,
- * src/source/op/kernels/cuda/mha_kernel.cu:178-341). */
+ * head map g(h) = h * kv_head_num / head_num (flash_decoding_kernel + combine,
+ * src/source/op/kernels/cuda/mha_kernel.cu:178-341). head_size <= 256, max_seq <= 2^24; *pos must
+ * be below max_seq (the cache rows 0..*pos are read). */
 int sq8_attention_decode(const float* q, const float* key_cache, const float* value_cache,
                          const int32_t* pos, float* out, int head_num, int kv_head_num,
                          int head_size, int max_seq, void* hip_stream);

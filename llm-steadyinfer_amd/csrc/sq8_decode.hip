@@ -158,27 +158,63 @@ struct RopeArgs {
 constexpr int kAttnBlock = 1024;
 constexpr int kAttnWaves = kAttnBlock / kWave;
 
+// One workgroup (16 waves) per query head, in a single memory round trip:
+//  * wave w owns the cache positions w, w + 16, w + 32, ...; lane l holds head dims l, l + 64,
+//    ... of their key and value rows. Those loads do not depend on anything computed here, so the
+//    first chunk of them is issued before the query is rotated and staged;
+//  * a score is the lanes' partial dot products summed across the wave; softmax runs online per
+//    wave (running max m, sum l and weighted value sum), so the positions need no LDS array and
+//    the only barriers are the query stage and the final combine of the 16 waves:
+//        M = max_w m_w,  out[d] = sum_w acc_w[d] exp(m_w - M) / sum_w l_w exp(m_w - M).
+//  * with ROPE the workgroup first rotates q and the token's k (pairs (i, i + hs/2) at table
+//    column 2i), the group's leader writes k and v to cache row pos, and the token's own position
+//    is scored from LDS (the cache rows read are 0 .. pos-1, written by earlier steps).
 template <int HS_MAX, bool ROPE>
 __global__ __launch_bounds__(kAttnBlock) void attention_decode_kernel(
-    const float* __restrict__ q, const float* __restrict__ kcache,
-    const float* __restrict__ vcache, const int32_t* __restrict__ pos_ptr,
-    float* __restrict__ out, int head_num, int kv_head_num, int head_size, RopeArgs ra) {
-  extern __shared__ float s_p[];  // [seq] scores, then probabilities
-  __shared__ float red[kAttnWaves];
+    const float* __restrict__ q, const float* kcache, const float* vcache,
+    const int32_t* __restrict__ pos_ptr, float* __restrict__ out, int head_num, int kv_head_num,
+    int head_size, RopeArgs ra) {
+  constexpr int DPL = HS_MAX / kWave;  // head dims per lane
+  constexpr int PCH = 4;               // cache positions per wave per chunk
+  constexpr int W = kAttnWaves;
   __shared__ __attribute__((aligned(16))) float s_q[HS_MAX];
   __shared__ float s_k[HS_MAX];
   __shared__ float s_v[HS_MAX];
-  __shared__ float s_part[kAttnWaves][HS_MAX];
-  constexpr int DPL = HS_MAX / kWave;  // head dims per lane in the value pass
+  __shared__ float s_m[W], s_l[W];
+  __shared__ float s_acc[W][HS_MAX];
   const int head = blockIdx.x;
   const int pos = *pos_ptr;
   const int seq = pos + 1;
   const int kv_dim = kv_head_num * head_size;
   const int group = head * kv_head_num / head_num;
   const int hoff = group * head_size;
-  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // Positions read from the cache: all of them, or all but pos when pos comes from registers.
   const int ncache = ROPE ? pos : seq;
+  const int nmine = wave < ncache ? (ncache - 1 - wave) / W + 1 : 0;
+  const int nch = (nmine + PCH - 1) / PCH;
+
+  // Chunk c of this wave's rows into register buffer b. Branch-free: positions past the wave's
+  // last (and dims past head_size) re-read a valid element and are never used.
+  float kr[2][PCH][DPL], vr[2][PCH][DPL];
+  const int tmax = max(ncache - 1, 0);
+  auto load = [&](int b, int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < PCH; ++i) {
+      const int t = min(wave + (c * PCH + i) * W, tmax);
+      const float* krow = kcache + static_cast<size_t>(t) * kv_dim + hoff;
+      const float* vrow = vcache + static_cast<size_t>(t) * kv_dim + hoff;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        const int d = min(lane + j * kWave, head_size - 1);
+        kr[b][i][j] = krow[d];
+        vr[b][i][j] = vrow[d];
+      }
+    }
+  };
+  if (nch > 0) load(0, 0);
+
   if (ROPE) {
     const int half = head_size / 2;
     const bool leader = head == (group * head_num + kv_head_num - 1) / kv_head_num;
@@ -210,91 +246,81 @@ __global__ __launch_bounds__(kAttnBlock) void attention_decode_kernel(
     for (int d = threadIdx.x; d < head_size; d += kAttnBlock) s_q[d] = q[head * head_size + d];
   }
   __syncthreads();
+
   const float scale = 1.f / sqrtf(static_cast<float>(head_size));
-  const bool vec4 = (head_size % 4) == 0 && (kv_dim % 4) == 0 && (hoff % 4) == 0;
-  for (int t = threadIdx.x; t < seq; t += kAttnBlock) {
-    float a0 = 0.f, a1 = 0.f;
-    if (ROPE && t == pos) {
-      for (int d = 0; d < head_size; ++d) a0 = fmaf(s_q[d], s_k[d], a0);
-    } else if (vec4) {
-      const float* krow = kcache + static_cast<size_t>(t) * kv_dim + hoff;
-#pragma unroll 8
-      for (int d = 0; d < head_size; d += 8) {
-        const float4 k0 = *reinterpret_cast<const float4*>(krow + d);
-        const float4 q0 = *reinterpret_cast<const float4*>(s_q + d);
-        a0 = fmaf(q0.x, k0.x, a0);
-        a0 = fmaf(q0.y, k0.y, a0);
-        a0 = fmaf(q0.z, k0.z, a0);
-        a0 = fmaf(q0.w, k0.w, a0);
-        if (d + 4 < head_size) {
-          const float4 k1 = *reinterpret_cast<const float4*>(krow + d + 4);
-          const float4 q1 = *reinterpret_cast<const float4*>(s_q + d + 4);
-          a1 = fmaf(q1.x, k1.x, a1);
-          a1 = fmaf(q1.y, k1.y, a1);
-          a1 = fmaf(q1.z, k1.z, a1);
-          a1 = fmaf(q1.w, k1.w, a1);
-        }
-      }
-    } else {
-      const float* krow = kcache + static_cast<size_t>(t) * kv_dim + hoff;
-      for (int d = 0; d < head_size; ++d) a0 = fmaf(s_q[d], krow[d], a0);
-    }
-    s_p[t] = (a0 + a1) * scale;
-  }
-  __syncthreads();
-  float m = -FLT_MAX;
-  for (int t = threadIdx.x; t < seq; t += kAttnBlock) m = fmaxf(m, s_p[t]);
-  m = block_max<kAttnWaves>(m, red);
-  float l = 0.f;
-  for (int t = threadIdx.x; t < seq; t += kAttnBlock) {
-    const float p = expf(s_p[t] - m);
-    s_p[t] = p;
-    l += p;
-  }
-  l = block_sum<kAttnWaves>(l, red);  // its barriers also publish the probabilities
-  float acc[DPL];
+  float qv[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j)
+    qv[j] = lane + j * kWave < head_size ? s_q[lane + j * kWave] : 0.f;
+  float m = -INFINITY, l = 0.f, acc[DPL];
 #pragma unroll
   for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
-  const float* vbase = vcache + hoff + lane;
-  constexpr int UNR = 8;
-  int t = wave;
-  for (; t + (UNR - 1) * kAttnWaves < ncache; t += UNR * kAttnWaves) {
-    float v[UNR][DPL];
+  auto consume = [&](float sc, const float (&v)[DPL]) __attribute__((always_inline)) {
+    const float mn = fmaxf(m, sc);
+    const float f = expf(m - mn), p = expf(sc - mn);
+    l = fmaf(l, f, p);
 #pragma unroll
-    for (int u = 0; u < UNR; ++u)
+    for (int j = 0; j < DPL; ++j) acc[j] = fmaf(acc[j], f, p * v[j]);
+    m = mn;
+  };
+  auto chunk = [&](int b, int c) __attribute__((always_inline)) {
+    float part[PCH];
 #pragma unroll
-      for (int j = 0; j < DPL; ++j)
-        v[u][j] = lane + j * kWave < head_size
-                      ? vbase[static_cast<size_t>(t + u * kAttnWaves) * kv_dim + j * kWave]
-                      : 0.f;
+    for (int i = 0; i < PCH; ++i) {
+      float a = 0.f;
 #pragma unroll
-    for (int u = 0; u < UNR; ++u) {
-      const float p = s_p[t + u * kAttnWaves];
-#pragma unroll
-      for (int j = 0; j < DPL; ++j) acc[j] = fmaf(p, v[u][j], acc[j]);
+      for (int j = 0; j < DPL; ++j) a = fmaf(qv[j], kr[b][i][j], a);
+      part[i] = a;
     }
-  }
-  for (; t < ncache; t += kAttnWaves) {
-    const float p = s_p[t];
 #pragma unroll
-    for (int j = 0; j < DPL; ++j)
-      if (lane + j * kWave < head_size)
-        acc[j] = fmaf(p, vbase[static_cast<size_t>(t) * kv_dim + j * kWave], acc[j]);
-  }
-  if (ROPE && wave == pos % kAttnWaves) {  // position pos from registers, in its wave's order
-    const float p = s_p[pos];
+    for (int off = 32; off >= 1; off /= 2)
 #pragma unroll
-    for (int j = 0; j < DPL; ++j)
-      if (lane + j * kWave < head_size) acc[j] = fmaf(p, s_v[lane + j * kWave], acc[j]);
+      for (int i = 0; i < PCH; ++i) part[i] += __shfl_xor(part[i], off, kWave);
+#pragma unroll
+    for (int i = 0; i < PCH; ++i)
+      if (c * PCH + i < nmine) consume(part[i] * scale, vr[b][i]);
+  };
+  // Register double buffer over chunks, the prefetch issued unconditionally (clamped index).
+  for (int c = 0; c < nch; c += 2) {
+    load(1, min(c + 1, nch - 1));
+    chunk(0, c);
+    if (c + 1 >= nch) break;
+    load(0, min(c + 2, nch - 1));
+    chunk(1, c + 1);
+  }
+  if (ROPE && wave == pos % W) {  // the token's own position, from LDS
+    float a = 0.f, v[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const int d = lane + j * kWave;
+      a = fmaf(qv[j], d < head_size ? s_k[d] : 0.f, a);
+      v[j] = d < head_size ? s_v[d] : 0.f;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off /= 2) a += __shfl_xor(a, off, kWave);
+    consume(a * scale, v);
+  }
+
+  if (lane == 0) {
+    s_m[wave] = m;
+    s_l[wave] = l;
   }
 #pragma unroll
-  for (int j = 0; j < DPL; ++j) s_part[wave][lane + j * kWave] = acc[j];
+  for (int j = 0; j < DPL; ++j)
+    if (lane + j * kWave < head_size) s_acc[wave][lane + j * kWave] = acc[j];
   __syncthreads();
-  for (int d = threadIdx.x; d < head_size; d += kAttnBlock) {
-    float o = s_part[0][d];
+  float mx = s_m[0];
 #pragma unroll
-    for (int w = 1; w < kAttnWaves; ++w) o += s_part[w][d];
-    out[head * head_size + d] = o / l;
+  for (int w = 1; w < W; ++w) mx = fmaxf(mx, s_m[w]);
+  for (int d = threadIdx.x; d < head_size; d += kAttnBlock) {
+    float o = 0.f, lt = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float f = s_m[w] == -INFINITY ? 0.f : expf(s_m[w] - mx);
+      o = fmaf(s_acc[w][d], f, o);
+      lt = fmaf(s_l[w], f, lt);
+    }
+    out[head * head_size + d] = o / lt;
   }
 }
 
@@ -499,11 +525,15 @@ int sq8_attention_decode(const float* q, const float* key_cache, const float* va
   if (head_num <= 0 || kv_head_num <= 0 || head_num % kv_head_num || head_size <= 0 ||
       head_size > 256 || max_seq <= 0)
     return SQ8_ERR_DIMS;
-  const size_t lds = static_cast<size_t>(max_seq) * sizeof(float);
-  if (lds > 40 * 1024) return SQ8_ERR_DIMS;  // scores of one head live in LDS (<= 10240 positions)
-  hipLaunchKernelGGL((attention_decode_kernel<256, false>), dim3(head_num), dim3(kAttnBlock), lds,
-                     stream_of(hip_stream), q, key_cache, value_cache, pos, out, head_num,
-                     kv_head_num, head_size, RopeArgs{});
+  if (max_seq > (1 << 24)) return SQ8_ERR_DIMS;
+  if (head_size <= 128)
+    hipLaunchKernelGGL((attention_decode_kernel<128, false>), dim3(head_num), dim3(kAttnBlock), 0,
+                       stream_of(hip_stream), q, key_cache, value_cache, pos, out, head_num,
+                       kv_head_num, head_size, RopeArgs{});
+  else
+    hipLaunchKernelGGL((attention_decode_kernel<256, false>), dim3(head_num), dim3(kAttnBlock), 0,
+                       stream_of(hip_stream), q, key_cache, value_cache, pos, out, head_num,
+                       kv_head_num, head_size, RopeArgs{});
   return launched();
 }
 
@@ -516,13 +546,17 @@ int sq8_rope_attention_decode(const float* qkv, int head_num, int kv_head_num, i
   if (head_num <= 0 || kv_head_num <= 0 || head_num % kv_head_num || head_size <= 0 ||
       head_size % 2 || head_size > 256 || max_seq <= 0)
     return SQ8_ERR_DIMS;
-  const size_t lds = static_cast<size_t>(max_seq) * sizeof(float);
-  if (lds > 40 * 1024) return SQ8_ERR_DIMS;
+  if (max_seq > (1 << 24)) return SQ8_ERR_DIMS;
   const RopeArgs ra{head_num * head_size, kv_head_num * head_size, sin_cache, cos_cache, key_cache,
                     value_cache};
-  hipLaunchKernelGGL((attention_decode_kernel<256, true>), dim3(head_num), dim3(kAttnBlock), lds,
-                     stream_of(hip_stream), qkv, key_cache, value_cache, pos, out, head_num,
-                     kv_head_num, head_size, ra);
+  if (head_size <= 128)
+    hipLaunchKernelGGL((attention_decode_kernel<128, true>), dim3(head_num), dim3(kAttnBlock), 0,
+                       stream_of(hip_stream), qkv, key_cache, value_cache, pos, out, head_num,
+                       kv_head_num, head_size, ra);
+  else
+    hipLaunchKernelGGL((attention_decode_kernel<256, true>), dim3(head_num), dim3(kAttnBlock), 0,
+                       stream_of(hip_stream), qkv, key_cache, value_cache, pos, out, head_num,
+                       kv_head_num, head_size, ra);
   return launched();
 }
 

@@ -18,7 +18,7 @@ def test_decode_ops_reject_bad_arguments(sq8):
     assert L.sq8_rope_kv(FAKE, 128, 256, 64, FAKE, FAKE, FAKE, FAKE, FAKE, 16, None) == sq8.SQ8_ERR_DIMS
     assert L.sq8_attention_decode(FAKE, FAKE, FAKE, FAKE, FAKE, 6, 4, 64, 16, None) == sq8.SQ8_ERR_DIMS
     assert L.sq8_attention_decode(FAKE, FAKE, FAKE, FAKE, FAKE, 8, 2, 512, 16, None) == sq8.SQ8_ERR_DIMS
-    assert L.sq8_attention_decode(FAKE, FAKE, FAKE, FAKE, FAKE, 8, 2, 64, 1 << 20, None) == sq8.SQ8_ERR_DIMS
+    assert L.sq8_attention_decode(FAKE, FAKE, FAKE, FAKE, FAKE, 8, 2, 64, 1 << 25, None) == sq8.SQ8_ERR_DIMS
     assert L.sq8_quantize(FAKE, 100, 64, FAKE, FAKE, None) == sq8.SQ8_ERR_GROUP
     assert L.sq8_argmax(FAKE, 0, FAKE, FAKE, 4096, None) == sq8.SQ8_ERR_DIMS
     assert L.sq8_argmax(FAKE, 5000, FAKE, FAKE, 8, None) == sq8.SQ8_ERR_WORKSPACE
