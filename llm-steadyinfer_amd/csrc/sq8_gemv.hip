@@ -152,6 +152,68 @@ struct ProArgs {
   float eps;
 };
 
+// Stage the token rows (or the fused prologue's result) in LDS for a workgroup of WV waves.
+// Token rows M .. MT-1 are staged as zeros. float4 number i is stored at i ^ ((i >> 4) & 3): a
+// lane reads the 4 float4 of its 16-element chunk, and without the swizzle lanes l and l+4 would
+// hit the same LDS banks in every ds_read_b128 (4-way conflicts). The caller's barrier publishes
+// the stage.
+template <int MT, int WV, int PRO>
+__device__ __forceinline__ void stage_x(const float* __restrict__ x, int M, int K,
+                                        const ProArgs& pro, float* xs) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+  float4* xs4 = reinterpret_cast<float4*>(xs);
+  if (PRO == kProNone) {
+    for (int i = tid; i < MT * K / 4; i += WV * kWave) {
+      const float4 v = i < M * K / 4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      xs4[i ^ ((i >> 4) & 3)] = v;
+    }
+  } else if (PRO == kProNorm) {
+    __shared__ float red[WV];
+    const float4* r4 = reinterpret_cast<const float4*>(pro.res);
+    float ss = 0.f;
+    for (int i = tid; i < K / 4; i += WV * kWave) {
+      float4 v = x4[i];
+      if (r4) {
+        const float4 r = r4[i];
+        v = make_float4(v.x + r.x, v.y + r.y, v.z + r.z, v.w + r.w);
+      }
+      ss = fmaf(v.x, v.x, ss);
+      ss = fmaf(v.y, v.y, ss);
+      ss = fmaf(v.z, v.z, ss);
+      ss = fmaf(v.w, v.w, ss);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off /= 2) ss += __shfl_xor(ss, off, kWave);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float total = red[0];
+#pragma unroll
+    for (int v = 1; v < WV; ++v) total += red[v];
+    const float scale = rsqrtf(total / static_cast<float>(K) + pro.eps);
+    const float4* n4 = reinterpret_cast<const float4*>(pro.nw);
+    float4* o4 = reinterpret_cast<float4*>(pro.x_out);
+    for (int i = tid; i < K / 4; i += WV * kWave) {
+      float4 v = x4[i];
+      if (r4) {
+        const float4 r = r4[i];
+        v = make_float4(v.x + r.x, v.y + r.y, v.z + r.z, v.w + r.w);
+      }
+      if (o4 && blockIdx.x == 0) o4[i] = v;
+      const float4 g = n4[i];
+      xs4[i ^ ((i >> 4) & 3)] = make_float4(scale * v.x * g.x, scale * v.y * g.y,
+                                            scale * v.z * g.z, scale * v.w * g.w);
+    }
+  } else {
+    for (int i = tid; i < K / 4; i += WV * kWave) {
+      const float4 a = x4[i], g = x4[K / 4 + i];
+      xs4[i ^ ((i >> 4) & 3)] = make_float4(silu_mul(a.x, g.x), silu_mul(a.y, g.y),
+                                            silu_mul(a.z, g.z), silu_mul(a.w, g.w));
+    }
+  }
+}
+
 template <int R, int U, int MT, int GS, bool TAIL, int WV = kWaves, int PRO = kProNone>
 __global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restrict__ x,
                                                          const int8_t* __restrict__ w,
@@ -209,59 +271,7 @@ __global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restri
     load_scales(b, 0, scn);
   }
 
-  // Token rows M .. MT-1 are staged as zeros. float4 number i is stored at i ^ ((i >> 4) & 3): a
-  // lane reads the 4 float4 of its 16-element chunk, and without the swizzle lanes l and l+4 would
-  // hit the same LDS banks in every ds_read_b128 (4-way conflicts).
-  const float4* x4 = reinterpret_cast<const float4*>(x);
-  float4* xs4 = reinterpret_cast<float4*>(xs);
-  if (PRO == kProNone) {
-    for (int i = tid; i < MT * K / 4; i += WV * kWave) {
-      const float4 v = i < M * K / 4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-      xs4[i ^ ((i >> 4) & 3)] = v;
-    }
-  } else if (PRO == kProNorm) {
-    __shared__ float red[WV];
-    const float4* r4 = reinterpret_cast<const float4*>(pro.res);
-    float ss = 0.f;
-    for (int i = tid; i < K / 4; i += WV * kWave) {
-      float4 v = x4[i];
-      if (r4) {
-        const float4 r = r4[i];
-        v = make_float4(v.x + r.x, v.y + r.y, v.z + r.z, v.w + r.w);
-      }
-      ss = fmaf(v.x, v.x, ss);
-      ss = fmaf(v.y, v.y, ss);
-      ss = fmaf(v.z, v.z, ss);
-      ss = fmaf(v.w, v.w, ss);
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off /= 2) ss += __shfl_xor(ss, off, kWave);
-    if (lane == 0) red[wave] = ss;
-    __syncthreads();
-    float total = red[0];
-#pragma unroll
-    for (int v = 1; v < WV; ++v) total += red[v];
-    const float scale = rsqrtf(total / static_cast<float>(K) + pro.eps);
-    const float4* n4 = reinterpret_cast<const float4*>(pro.nw);
-    float4* o4 = reinterpret_cast<float4*>(pro.x_out);
-    for (int i = tid; i < K / 4; i += WV * kWave) {
-      float4 v = x4[i];
-      if (r4) {
-        const float4 r = r4[i];
-        v = make_float4(v.x + r.x, v.y + r.y, v.z + r.z, v.w + r.w);
-      }
-      if (o4 && blockIdx.x == 0) o4[i] = v;
-      const float4 g = n4[i];
-      xs4[i ^ ((i >> 4) & 3)] = make_float4(scale * v.x * g.x, scale * v.y * g.y,
-                                            scale * v.z * g.z, scale * v.w * g.w);
-    }
-  } else {
-    for (int i = tid; i < K / 4; i += WV * kWave) {
-      const float4 a = x4[i], g = x4[K / 4 + i];
-      xs4[i ^ ((i >> 4) & 3)] = make_float4(silu_mul(a.x, g.x), silu_mul(a.y, g.y),
-                                            silu_mul(a.z, g.z), silu_mul(a.w, g.w));
-    }
-  }
+  stage_x<MT, WV, PRO>(x, M, K, pro, xs);
   __syncthreads();
   if constexpr (!kEarly) load_scales(b, 0, scn);
 
@@ -312,6 +322,73 @@ __global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restri
   while (b < nblk) {
     load_w(b, st, q);
     step();
+  }
+}
+
+// Single-token GEMV for few, long rows (N small, K >= 8 KiB): a workgroup of WV waves owns
+// WV/KS rows and the KS waves of a row split its 1 KiB chunks (wave part p takes chunks p, p + KS,
+// ..., so neighbouring waves read neighbouring pieces of the row). A wave requests all of its U
+// chunks (and their scales) at once, then the row's KS partial sums are added in LDS in part
+// order. With one row per wave, such a shape leaves most of the chip idle and every wave walks
+// its row in several dependent round trips.
+template <int U, int KS, int WV, int GS, bool TAIL, int PRO>
+__global__ __launch_bounds__(WV * kWave) void splitrow_kernel(const float* __restrict__ x,
+                                                            const int8_t* __restrict__ w,
+                                                            const float* __restrict__ s,
+                                                            float* __restrict__ y, int N, int K,
+                                                            int gs_rt, ProArgs pro) {
+  static_assert(WV % KS == 0, "whole rows per workgroup");
+  constexpr int RW = WV / KS;
+  extern __shared__ float xs[];
+  __shared__ float part[WV];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rw = wave / KS, p = wave % KS;
+  const int nr = min(blockIdx.x * RW + rw, N - 1);
+  const int gs = GS ? GS : gs_rt;
+  const int8_t* wrow = w + static_cast<size_t>(nr) * K;
+  const float* srow = s + static_cast<size_t>(nr) * (K / gs);
+  i32x4 q[U];
+  float sc[U];
+  // Chunks past the row end (TAIL) read the row's first chunk and are dropped at use.
+  auto issue = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = (p + KS * u) * 1024 + lane * 16;
+      const int kc = !TAIL || k < K ? k : 0;
+      q[u] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(wrow + kc));
+      sc[u] = srow[kc / gs];
+    }
+  };
+  // Behind a fused prologue the weights are requested first (their latency overlaps the
+  // staging); with a plain copy of x they follow it, as in sweep_kernel.
+  constexpr bool kEarly = PRO != kProNone;
+  if constexpr (kEarly) issue();
+  stage_x<1, WV, PRO>(x, 1, K, pro, xs);
+  __syncthreads();
+  if constexpr (!kEarly) issue();
+  float acc = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int k = (p + KS * u) * 1024 + lane * 16;
+    const bool ok = !TAIL || k < K;
+    const int i0 = (ok ? k : 0) / 4;
+    const float4* xp = reinterpret_cast<const float4*>(xs) + i0;
+    const int sw = (i0 >> 4) & 3;
+    const float4 x0 = xp[0 ^ sw], x1 = xp[1 ^ sw], x2 = xp[2 ^ sw], x3 = xp[3 ^ sw];
+    const float d = dot16(q[u], x0, x1, x2, x3);
+    acc = fmaf(ok ? sc[u] : 0.f, d, acc);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off /= 2) acc += __shfl_xor(acc, off, kWave);
+  if (lane == 0) part[wave] = acc;
+  __syncthreads();
+  if (tid < RW) {
+    float v = part[tid * KS];
+#pragma unroll
+    for (int i = 1; i < KS; ++i) v += part[tid * KS + i];
+    const int n = blockIdx.x * RW + tid;
+    if (n < N) y[n] = v;
   }
 }
 
@@ -410,9 +487,36 @@ hipError_t launch_sweep(const float* x, const int8_t* w, const float* s, float* 
 // a step covers the row in at most 4 iterations of 1 KiB, so short rows (1.5 KiB) do not issue
 // masked loads; up to 8192 rows one row per wave in 8-wave workgroups, more rows 2 rows per wave
 // in 4-wave workgroups.
+// Split-row GEMV (M = 1): KS waves per row, U chunks of 1 KiB per wave, WV waves per workgroup.
+template <int U, int KS, int WV, int PRO>
+hipError_t launch_splitrow(const float* x, const int8_t* w, const float* s, float* y, int N, int K,
+                           int gs, hipStream_t st, const ProArgs& pro) {
+  const size_t lds = static_cast<size_t>(K) * sizeof(float);
+  const dim3 grid((N + WV / KS - 1) / (WV / KS));
+  const bool tail = K != KS * U * 1024;
+  if (gs == 64) {
+    if (tail)
+      hipLaunchKernelGGL((splitrow_kernel<U, KS, WV, 64, true, PRO>), grid, dim3(WV * kWave), lds,
+                         st, x, w, s, y, N, K, gs, pro);
+    else
+      hipLaunchKernelGGL((splitrow_kernel<U, KS, WV, 64, false, PRO>), grid, dim3(WV * kWave), lds,
+                         st, x, w, s, y, N, K, gs, pro);
+  } else {
+    hipLaunchKernelGGL((splitrow_kernel<U, KS, WV, 0, true, PRO>), grid, dim3(WV * kWave), lds, st,
+                       x, w, s, y, N, K, gs, pro);
+  }
+  return hipGetLastError();
+}
+
 template <int MT, int PRO = kProNone>
 hipError_t launch_stream(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
                          int K, int gs, hipStream_t st, const ProArgs& pro = {}) {
+  // Few long rows behind a fused prologue (Qwen2-1.5B down projection: 1536 rows of 8.75 KiB):
+  // two waves per row, 8 rows per 16-wave workgroup. The prologue is recomputed by every
+  // workgroup, so the workgroup count stays that of one row per wave in 8-wave workgroups (with
+  // 8-wave split-row workgroups, twice as many, the decode step measured slower).
+  if (MT == 1 && PRO != kProNone && N <= 2048 && K >= 8192 && K <= 10 * 1024)
+    return launch_splitrow<5, 2, 16, PRO>(x, w, s, y, N, K, gs, st, pro);
   if (K >= 8192) {
     return K % 7168 == 0 ? launch_sweep<1, 7, 16, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro)
                          : launch_sweep<1, 4, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
