@@ -209,7 +209,7 @@ def test_matmul_rmsnorm_equals_separate_ops(sq8, dev, N, K, with_res):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("N,K", [(1536, 8960), (4096, 14336), (64, 1024)])
+@pytest.mark.parametrize("N,K", [(1536, 8960), (1001, 10240), (2048, 8256), (4096, 14336), (64, 1024)])
 def test_matmul_swiglu_equals_separate_ops(sq8, dev, N, K):
     import torch
     rng = np.random.default_rng(K)
