@@ -19,6 +19,8 @@
 // 16-term fp32 dot product. The R x MT partial sums of a lane are reduced across the wave with a
 // reduce-scatter butterfly (R*MT values in log2(R*MT) exchange rounds instead of 6 rounds each),
 // then across the 4 waves through LDS in a fixed order, so results are deterministic.
+#include <cmath>
+
 #include "sq8_common.h"
 
 namespace sq8 {
@@ -529,6 +531,15 @@ hipError_t launch_stream(const float* x, const int8_t* w, const float* s, float*
   }
   if (u == 1) return launch_sweep<2, 1, 4, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
   if (u == 2) return launch_sweep<2, 2, 4, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
+  if (PRO == kProNone && MT == 1) {
+    // One row per wave when that spreads the row blocks more evenly over the 16 waves per CU
+    // (Llama gate/up: 28672 rows = exactly 7 per wave, against 3.5 two-row blocks: +1 % on the
+    // decode step).
+    const double waves = 16.0 * cu_count();
+    const double b1 = N / waves, b2 = N / (2.0 * waves);
+    if (b1 / std::ceil(b1) > b2 / std::ceil(b2) + 0.01)
+      return launch_sweep<1, 4, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
+  }
   return launch_sweep<2, 4, 4, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
 }
 
