@@ -27,6 +27,8 @@ DECODE_SYMBOLS = ("sq8_embedding", "sq8_rmsnorm", "sq8_add_rmsnorm", "sq8_rope_t
                   "sq8_attention_decode", "sq8_swiglu", "sq8_add", "sq8_argmax_workspace_bytes",
                   "sq8_argmax", "sq8_quantize", "sq8_step_advance", "sq8_matmul_rmsnorm",
                   "sq8_matmul_swiglu", "sq8_rope_attention_decode")
+# include/sq8_batch.h
+BATCH_SYMBOLS = ("sq8_paged_rope_kv", "sq8_paged_attention", "sq8_swiglu_rows", "sq8_argmax_rows")
 
 _lib = None
 
@@ -70,6 +72,10 @@ def lib() -> ctypes.CDLL:
             "sq8_matmul_rmsnorm": [vp, vp, vp, vp, f32, vp, vp, vp, I, I, I, vp],
             "sq8_matmul_swiglu": [vp, vp, vp, vp, I, I, I, vp],
             "sq8_rope_attention_decode": [vp, I, I, I, vp, vp, vp, vp, vp, vp, I, vp],
+            "sq8_paged_rope_kv": [vp, I, I, I, I, vp, vp, I, I, vp, vp, vp, vp, vp],
+            "sq8_paged_attention": [vp, I, I, I, I, I, vp, vp, I, I, vp, vp, vp, vp],
+            "sq8_swiglu_rows": [vp, I, I, vp, vp],
+            "sq8_argmax_rows": [vp, I, I, vp, vp],
         }
         for name, args in sigs.items():
             fn = getattr(L, name)
@@ -247,3 +253,38 @@ def rope_attention_decode(qkv, head_num: int, kv_head_num: int, head_size: int, 
     _call("sq8_rope_attention_decode", _ptr(qkv), head_num, kv_head_num, head_size, _ptr(pos),
           _ptr(sin_cache), _ptr(cos_cache), _ptr(kcache), _ptr(vcache), _ptr(out), max_seq,
           stream=stream)
+
+
+# Thin wrappers over include/sq8_batch.h (continuous batching, paged KV cache).
+
+
+def paged_rope_kv(qkv, head_num: int, kv_head_num: int, head_size: int, positions, block_table,
+                  block_size: int, sin_cache, cos_cache, kcache, vcache, stream=None):
+    """Rows of qkv ([rows][dim + 2 kv_dim]) at their positions: rotate q in place, write the
+    rotated k and v to the rows' paged cache slots. positions int32 [rows], block_table int32
+    [rows][stride]; kcache/vcache [num_blocks][block_size][kv_dim] of one layer."""
+    rows = positions.numel()
+    _call("sq8_paged_rope_kv", _ptr(qkv), rows, head_num, kv_head_num, head_size, _ptr(positions),
+          _ptr(block_table), block_table.shape[-1], block_size, _ptr(sin_cache), _ptr(cos_cache),
+          _ptr(kcache), _ptr(vcache), stream=stream)
+
+
+def paged_attention(qkv, q_stride: int, head_num: int, kv_head_num: int, head_size: int,
+                    positions, block_table, block_size: int, kcache, vcache, out, stream=None):
+    """out[r] = attention of row r's query heads over positions 0..positions[r] of its sequence."""
+    rows = positions.numel()
+    _call("sq8_paged_attention", _ptr(qkv), q_stride, rows, head_num, kv_head_num, head_size,
+          _ptr(positions), _ptr(block_table), block_table.shape[-1], block_size, _ptr(kcache),
+          _ptr(vcache), _ptr(out), stream=stream)
+
+
+def swiglu_rows(gate_up, out, stream=None):
+    """out[r][i] = silu(gate_up[r][i]) * gate_up[r][ffn + i]."""
+    rows, two_ffn = gate_up.shape
+    _call("sq8_swiglu_rows", _ptr(gate_up), rows, two_ffn // 2, _ptr(out), stream=stream)
+
+
+def argmax_rows(logits, out, stream=None):
+    """out[r] = first maximum of logits[r] (int32 on the device)."""
+    rows, n = logits.shape
+    _call("sq8_argmax_rows", _ptr(logits), rows, n, _ptr(out), stream=stream)

@@ -1,0 +1,130 @@
+"""Batched forward over a paged KV cache on gfx950: the reference's forward_batch
+(src/source/model/llama3.cpp:996-1194) for rows of many sequences, each at its own position, as
+the continuous-batching scheduler (scheduler.py) hands them over. Every launch goes to
+libsq8.so (the INT8 matmul, include/sq8_decode.h and include/sq8_batch.h); torch supplies
+device memory only.
+
+Per step, for the B rows (decode rows first):
+    embedding -> per layer: [add +] RMSNorm (rows) -> fused QKV matmul (M = B) ->
+    paged RoPE + KV write (every row's k, v at its position) -> paged attention (row r over
+    positions 0 .. pos[r] of its sequence) -> O matmul -> add + RMSNorm -> fused gate/up matmul ->
+    SwiGLU (rows) -> down matmul
+    -> add + final RMSNorm -> classifier matmul on the decode rows only -> argmax per row.
+
+All rows write their KV before any row attends, so prefill rows of one sequence in the same step
+see each other causally. The KV pool is [layers][num_blocks][block_size][kv_dim] fp32 for keys
+and for values (KVManager's paged layout, src/source/scheduler/kv_manager.cpp).
+"""
+from __future__ import annotations
+
+from typing import List
+
+import numpy as np
+
+from . import (Workspace, add_rmsnorm, argmax_rows, embedding, matmul, paged_attention,
+               paged_rope_kv, rmsnorm, rope_tables, swiglu_rows)
+
+EPS = 1e-6
+
+
+class PagedBatchModel:
+    def __init__(self, cfg, weights: dict, group_size: int, max_rows: int, max_seq_len: int,
+                 num_blocks: int, block_size: int, device="cuda"):
+        import torch
+        self.torch = torch
+        self.cfg, self.w, self.gs = cfg, weights, group_size
+        self.max_rows, self.block_size = max_rows, block_size
+        self.max_blocks_per_seq = (max_seq_len + block_size - 1) // block_size
+        self.hs = cfg.dim // cfg.head_num
+        L, d, kv, h = cfg.layer_num, cfg.dim, cfg.kv_dim, cfg.hidden_dim
+        f32 = dict(dtype=torch.float32, device=device)
+        i32 = dict(dtype=torch.int32, device=device)
+        self.kcache = torch.zeros((L, num_blocks, block_size, kv), **f32)
+        self.vcache = torch.zeros((L, num_blocks, block_size, kv), **f32)
+        self.sin = torch.empty((max_seq_len, self.hs), **f32)
+        self.cos = torch.empty((max_seq_len, self.hs), **f32)
+        rope_tables(self.sin, self.cos, self.hs, max_seq_len, float(cfg.rope_theta))
+        R = max_rows
+        self.x = torch.zeros((R, d), **f32)
+        self.xn = torch.zeros((R, d), **f32)
+        self.qkv = torch.zeros((R, d + 2 * kv), **f32)
+        self.att = torch.zeros((R, d), **f32)
+        self.proj = torch.zeros((R, d), **f32)
+        self.gu = torch.zeros((R, 2 * h), **f32)
+        self.hid = torch.zeros((R, h), **f32)
+        self.logits = torch.zeros((R, cfg.vocab), **f32)
+        self.tok = torch.zeros(R, **i32)
+        self.pos = torch.zeros(R, **i32)
+        self.table = torch.zeros((R, self.max_blocks_per_seq), **i32)
+        self.next = torch.zeros(R, **i32)
+        self.ws = Workspace(device)
+        self.rows_run = 0
+
+    @classmethod
+    def from_decoder(cls, dec, max_rows: int, max_seq_len: int, num_blocks: int,
+                     block_size: int) -> "PagedBatchModel":
+        """Share the fused weights of an Int8Decoder (model file or random init)."""
+        return cls(dec.cfg, dec.w, dec.gs, max_rows, max_seq_len, num_blocks, block_size,
+                   dec.device)
+
+    def kv_bytes_per_position(self) -> int:
+        return 2 * 4 * self.cfg.layer_num * self.cfg.kv_dim
+
+    def _mm(self, x, qs, y, stream):
+        q, s = qs
+        matmul(x, q, s, y, group_size=self.gs, workspace=self.ws, stream=stream)
+
+    def forward(self, rows, tables: List[List[int]]) -> List[int]:
+        """Run the batch rows (scheduler.BatchRow, decode rows first) and return the greedy token
+        of each decode row."""
+        torch = self.torch
+        B = len(rows)
+        if B == 0 or B > self.max_rows:
+            raise ValueError(f"{B} rows for a model sized for {self.max_rows}")
+        nd = sum(1 for r in rows if r.is_decode)
+        tok = np.fromiter((r.token for r in rows), np.int32, B)
+        pos = np.fromiter((r.position for r in rows), np.int32, B)
+        tab = np.asarray(tables, np.int32).reshape(B, -1)
+        if tab.shape[1] != self.max_blocks_per_seq:
+            raise ValueError("block-table width does not match max_seq_len / block_size")
+        self.tok[:B].copy_(torch.from_numpy(tok))
+        self.pos[:B].copy_(torch.from_numpy(pos))
+        self.table[:B].copy_(torch.from_numpy(tab))
+        stream = torch.cuda.current_stream()
+        self.launch(B, nd, stream)
+        self.rows_run += B
+        if nd == 0:
+            return []
+        return self.next[:nd].cpu().tolist()
+
+    def launch(self, B: int, nd: int, stream) -> None:
+        """Enqueue the forward of the first B staged rows (tokens, positions and block tables in
+        self.tok / self.pos / self.table); writes the greedy tokens of the first nd rows to
+        self.next."""
+        cfg, w = self.cfg, self.w
+        L, d, kv = cfg.layer_num, cfg.dim, cfg.kv_dim
+        x, xn, qkv, att = self.x[:B], self.xn[:B], self.qkv[:B], self.att[:B]
+        proj, gu, hid = self.proj[:B], self.gu[:B], self.hid[:B]
+        pos, table = self.pos[:B], self.table[:B]
+        embedding(w["emb"], self.tok[:B], x, stream=stream)
+        for l in range(L):
+            if l == 0:
+                rmsnorm(x, w["norm"][0], xn, EPS, stream=stream)
+            else:  # residual of the previous FFN, then this layer's attention norm
+                add_rmsnorm(x, proj, w["norm"][l], xn, EPS, stream=stream)
+            self._mm(xn, w["qkv"][l], qkv, stream)
+            paged_rope_kv(qkv, cfg.head_num, cfg.kv_head_num, self.hs, pos, table,
+                          self.block_size, self.sin, self.cos, self.kcache[l], self.vcache[l],
+                          stream=stream)
+            paged_attention(qkv, d + 2 * kv, cfg.head_num, cfg.kv_head_num, self.hs, pos, table,
+                            self.block_size, self.kcache[l], self.vcache[l], att, stream=stream)
+            self._mm(att, w["o"][l], proj, stream)
+            add_rmsnorm(x, proj, w["norm"][L + l], xn, EPS, stream=stream)
+            self._mm(xn, w["gu"][l], gu, stream)
+            swiglu_rows(gu, hid, stream=stream)
+            self._mm(hid, w["down"][l], proj, stream)
+        if nd > 0:
+            add_rmsnorm(self.x[:nd], self.proj[:nd], w["norm"][2 * L], self.xn[:nd], EPS,
+                        stream=stream)
+            self._mm(self.xn[:nd], w["cls"], self.logits[:nd], stream)
+            argmax_rows(self.logits[:nd], self.next[:nd], stream=stream)
