@@ -21,7 +21,13 @@ INT8 model (28 layers, hidden 1536, 12 Q / 2 KV heads, FFN 8960, vocab 151936) d
 greedy tokens at batch 1 after a 64-token prompt, on the HIP decode stack (decoder.py), each token
 one HIP-graph replay; `--no-decode` skips it.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu] [--no-decode] [--graph]
+Config 5 (continuous batching): 64 requests with lognormal prompt lengths (median 200) on the
+Llama-3-8B-shaped model (the step's weights plus a random embedding), 128 greedy tokens each,
+through the paged-KV scheduler (scheduler.py) and batched model (batch_model.py): output
+tokens/s over the wall time of the whole run; `--no-batch` skips it.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu] [--no-decode]
+                       [--no-batch] [--graph]
        python bench.py --profile   # short run for rocprofv3 counter passes (see profiles/)
 """
 from __future__ import annotations
@@ -167,6 +173,64 @@ def decode_run(torch, n_prompt: int = 64, n_new: int = 128, seed: int = 0):
             "first_tokens": toks[:8].cpu().tolist()}
 
 
+def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed: int = 0,
+              sigma: float = 0.8):
+    """Config 5: continuous batching of n_seqs requests on the Llama-3-8B-shaped INT8 model (the
+    step's random-init projections, plus a random embedding and unit norms). Prompt lengths are
+    lognormal with median 200 (sigma 0.8, clipped to 16..2048), uniform random token ids,
+    n_new greedy tokens each, paged KV with block size 16 (the reference's choice for a mean
+    prompt of 64..1024), at most 64 running sequences and 64 rows per step (the reference's
+    max_batch). Eager launches; every step syncs once for its greedy tokens."""
+    import importlib
+    import numpy as np
+    mf = importlib.import_module("llm_steadyinfer_amd.model_file")
+    sch = importlib.import_module("llm_steadyinfer_amd.scheduler")
+    bm = importlib.import_module("llm_steadyinfer_amd.batch_model")
+    cfg = mf.LLAMA3_8B
+    dev = lm_head[0].device
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed + 77)
+    w = {"qkv": weights["qkv"], "o": weights["o"], "gu": weights["gate_up"],
+         "down": weights["down"], "cls": lm_head,
+         "emb": torch.randn((cfg.vocab, cfg.dim), generator=gen, device=dev),
+         "norm": [torch.ones(cfg.dim, device=dev) for _ in range(2 * cfg.layer_num + 1)]}
+    rng = np.random.default_rng(seed)
+    lens = np.clip(np.rint(np.exp(rng.normal(np.log(200.0), sigma, n_seqs))), 16, 2048)
+    prompts = [rng.integers(0, cfg.vocab, int(n)).tolist() for n in lens]
+    max_seq = int(lens.max()) + n_new
+    block = sch.Scheduler.resolve_block_size(float(lens.mean()))
+    s = sch.Scheduler(None, max_batch=64, max_seq_len=max_seq, max_gen_len=n_new,
+                      block_size=block)
+    model = bm.PagedBatchModel(cfg, w, GS, max_rows=64, max_seq_len=max_seq,
+                               num_blocks=s.alloc.num_blocks, block_size=block, device=dev)
+    s.forward = model.forward
+    for p in ([5, 6, 7], [8, 9]):          # warm-up requests (every kernel once), not timed
+        s.add_request(p)
+    s.run()
+    s.finished.clear()
+    steps0, rows0 = s.steps, s.rows_run
+    for p in prompts:
+        s.add_request(p)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    done = s.run()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gen_tokens = sum(len(q.generated_tokens) for q in done)
+    prompt_tokens = int(lens.sum())
+    return {"workload": f"config 5: Llama-3-8B-shaped random-init INT8 model, {n_seqs} sequences, "
+                        f"lognormal prompts (median 200, sigma {sigma}, clipped 16..2048; "
+                        f"mean {lens.mean():.0f}, max {int(lens.max())}), {n_new} greedy tokens "
+                        f"each, paged KV block {block}, max_batch 64",
+            "output_tokens_per_s": round(gen_tokens / wall, 1),
+            "total_tokens_per_s": round((gen_tokens + prompt_tokens) / wall, 1),
+            "wall_s": round(wall, 3), "generated_tokens": gen_tokens,
+            "prompt_tokens": prompt_tokens, "steps": s.steps - steps0,
+            "rows": s.rows_run - rows0, "preemptions": s.preemptions,
+            "kv_pool_GB": round(2 * 4 * cfg.layer_num * cfg.kv_dim * block * s.alloc.num_blocks
+                                / 1e9, 2),
+            "launch": "eager, one host sync per step"}
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -175,6 +239,7 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-batch", action="store_true", help="skip config 5 (continuous batching)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--graph", action="store_true", help="replay the step as one HIP graph")
     ap.add_argument("--profile", action="store_true",
@@ -275,8 +340,8 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": round(bytes_per_launch * GEMV_TRAFFIC_RATIO),
-                "kernel": "sq8 sweep_kernel, M=1 decode GEMV (<2,4,1,64> for K=4096, "
-                          "<2,2,1,64> for K=14336)",
+                "kernel": "sq8 sweep_kernel, M=1 decode GEMV (per-shape configurations: "
+                          "csrc/sq8_gemv.hip launch_stream)",
                 "avg_launch_us": round(launch_us, 3),
                 "algo_bytes_per_launch": round(bytes_per_launch)}
 
@@ -312,6 +377,12 @@ def main():
         decode = decode_run(torch)
         print(f"# decode done: {decode['tokens_per_s']} tokens/s", file=sys.stderr, flush=True)
 
+    batch = None
+    if not args.no_batch:
+        batch = batch_run(torch, weights, lm_head)
+        print(f"# batch done: {batch['output_tokens_per_s']} output tokens/s", file=sys.stderr,
+              flush=True)
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(torch, weights, args.cpu_seconds)
@@ -330,6 +401,8 @@ def main():
         "decode_matmul_tokens_per_s": round(1.0 / dt, 1),
         "decode_tokens_per_s": decode["tokens_per_s"] if decode else None,
         "decode": decode,
+        "batch_output_tokens_per_s": batch["output_tokens_per_s"] if batch else None,
+        "batch": batch,
         "step_algo_bytes": step_bytes,
         "roofline": roofline,
         "cpu_baseline": cpu,
