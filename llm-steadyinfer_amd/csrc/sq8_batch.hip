@@ -183,21 +183,34 @@ __device__ __forceinline__ bool first_max_better(float v, int i, float bv, int b
   return v > bv || (v == bv && i < bi);
 }
 
-// One workgroup per row: strided scan keeping the first maximum, then a wave and workgroup
-// reduction that prefers the smaller index on ties. NaN never compares greater.
-__global__ __launch_bounds__(kBlock) void argmax_rows_kernel(const float* __restrict__ logits,
-                                                             int n, int32_t* __restrict__ out) {
-  __shared__ float sv[kBlock / kWave];
-  __shared__ int si[kBlock / kWave];
+// One workgroup (kArgBlock threads) per row: strided float4 scan keeping the first maximum, then a
+// wave and workgroup reduction that prefers the smaller index on ties. NaN never compares greater.
+constexpr int kArgBlock = 1024;
+__global__ __launch_bounds__(kArgBlock) void argmax_rows_kernel(const float* __restrict__ logits,
+                                                                int n, int32_t* __restrict__ out) {
+  __shared__ float sv[kArgBlock / kWave];
+  __shared__ int si[kArgBlock / kWave];
   const float* row = logits + static_cast<size_t>(blockIdx.x) * n;
   float best = -INFINITY;
   int bi = INT_MAX;
-  for (int i = threadIdx.x; i < n; i += kBlock) {
-    const float v = row[i];
+  auto take = [&](float v, int i) __attribute__((always_inline)) {
     if (v > best || (bi == INT_MAX && v == best)) {
       best = v;
       bi = i;
     }
+  };
+  const bool vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0;
+  if (vec) {
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    for (int i = threadIdx.x; i < n / 4; i += kArgBlock) {
+      const float4 v = r4[i];
+      take(v.x, 4 * i);
+      take(v.y, 4 * i + 1);
+      take(v.z, 4 * i + 2);
+      take(v.w, 4 * i + 3);
+    }
+  } else {
+    for (int i = threadIdx.x; i < n; i += kArgBlock) take(row[i], i);
   }
 #pragma unroll
   for (int off = 32; off >= 1; off /= 2) {
@@ -215,7 +228,7 @@ __global__ __launch_bounds__(kBlock) void argmax_rows_kernel(const float* __rest
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < kBlock / kWave; ++w)
+    for (int w = 1; w < kArgBlock / kWave; ++w)
       if (first_max_better(sv[w], si[w], best, bi)) {
         best = sv[w];
         bi = si[w];
@@ -281,8 +294,8 @@ int sq8_swiglu_rows(const float* gate_up, int rows, int ffn, float* out, void* h
 int sq8_argmax_rows(const float* logits, int rows, int n, int32_t* out, void* hip_stream) {
   if (!logits || !out) return SQ8_ERR_NULL;
   if (rows <= 0 || n <= 0) return SQ8_ERR_DIMS;
-  hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(kBlock), 0, stream_of(hip_stream), logits,
-                     n, out);
+  hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(kArgBlock), 0, stream_of(hip_stream),
+                     logits, n, out);
   return launched();
 }
 

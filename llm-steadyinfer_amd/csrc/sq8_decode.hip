@@ -92,6 +92,71 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(float* __restrict__ x,
   for (int d = threadIdx.x; d < dim; d += kBlock) orow[d] = scale * xr[d] * w[d];
 }
 
+// The same for dim % 4 == 0 and dim <= 4 * NPT * kBlock: each thread keeps its NPT float4 of the
+// row in registers, so the row is read once and written once.
+template <bool ADD, int NPT>
+__global__ __launch_bounds__(kBlock) void rmsnorm_vec_kernel(float* __restrict__ x,
+                                                             const float* __restrict__ res,
+                                                             const float* __restrict__ w,
+                                                             float* __restrict__ out, int dim,
+                                                             float eps) {
+  __shared__ float red[kBlockWaves];
+  const int n4 = dim / 4;
+  float4* xr = reinterpret_cast<float4*>(x + static_cast<size_t>(blockIdx.x) * dim);
+  const float4* rr = reinterpret_cast<const float4*>(res + (ADD ? static_cast<size_t>(blockIdx.x) * dim : 0));
+  const float4* w4 = reinterpret_cast<const float4*>(w);
+  float4* orow = reinterpret_cast<float4*>(out + static_cast<size_t>(blockIdx.x) * dim);
+  float4 v[NPT];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < NPT; ++k) {
+    const int i = threadIdx.x + k * kBlock;
+    v[k] = i < n4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (ADD && i < n4) {
+      const float4 r = rr[i];
+      v[k] = make_float4(v[k].x + r.x, v[k].y + r.y, v[k].z + r.z, v[k].w + r.w);
+    }
+    ss = fmaf(v[k].x, v[k].x, ss);
+    ss = fmaf(v[k].y, v[k].y, ss);
+    ss = fmaf(v[k].z, v[k].z, ss);
+    ss = fmaf(v[k].w, v[k].w, ss);
+  }
+  const float total = block_sum(ss, red);
+  const float scale = rsqrtf(total / static_cast<float>(dim) + eps);
+#pragma unroll
+  for (int k = 0; k < NPT; ++k) {
+    const int i = threadIdx.x + k * kBlock;
+    if (i < n4) {
+      if (ADD) xr[i] = v[k];
+      const float4 g = w4[i];
+      orow[i] = make_float4(scale * v[k].x * g.x, scale * v[k].y * g.y, scale * v[k].z * g.z,
+                            scale * v[k].w * g.w);
+    }
+  }
+}
+
+template <bool ADD>
+void launch_rmsnorm(float* x, const float* res, const float* w, float* out, int rows, int dim,
+                    float eps, hipStream_t st) {
+  const bool vec = dim % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+                   (!ADD || (reinterpret_cast<uintptr_t>(res) & 15) == 0);
+  const int n4 = dim / 4;
+  if (vec && n4 <= kBlock)
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<ADD, 1>), dim3(rows), dim3(kBlock), 0, st, x, res, w,
+                       out, dim, eps);
+  else if (vec && n4 <= 4 * kBlock)
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<ADD, 4>), dim3(rows), dim3(kBlock), 0, st, x, res, w,
+                       out, dim, eps);
+  else if (vec && n4 <= 16 * kBlock)
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<ADD, 16>), dim3(rows), dim3(kBlock), 0, st, x, res, w,
+                       out, dim, eps);
+  else
+    hipLaunchKernelGGL((rmsnorm_kernel<ADD>), dim3(rows), dim3(kBlock), 0, st, x, res, w, out,
+                       dim, eps);
+}
+
 __global__ void rope_tables_kernel(float* __restrict__ sin_cache, float* __restrict__ cos_cache,
                                    int head_size, int max_seq, float theta) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
@@ -480,8 +545,8 @@ int sq8_rmsnorm(const float* x, const float* w, float* out, int rows, int dim, f
                 void* hip_stream) {
   if (!x || !w || !out) return SQ8_ERR_NULL;
   if (rows <= 0 || dim <= 0) return SQ8_ERR_DIMS;
-  hipLaunchKernelGGL((rmsnorm_kernel<false>), dim3(rows), dim3(kBlock), 0, stream_of(hip_stream),
-                     const_cast<float*>(x), nullptr, w, out, dim, eps);
+  launch_rmsnorm<false>(const_cast<float*>(x), nullptr, w, out, rows, dim, eps,
+                        stream_of(hip_stream));
   return launched();
 }
 
@@ -489,8 +554,7 @@ int sq8_add_rmsnorm(float* x, const float* res, const float* w, float* out, int 
                     float eps, void* hip_stream) {
   if (!x || !res || !w || !out) return SQ8_ERR_NULL;
   if (rows <= 0 || dim <= 0) return SQ8_ERR_DIMS;
-  hipLaunchKernelGGL((rmsnorm_kernel<true>), dim3(rows), dim3(kBlock), 0, stream_of(hip_stream),
-                     x, res, w, out, dim, eps);
+  launch_rmsnorm<true>(x, res, w, out, rows, dim, eps, stream_of(hip_stream));
   return launched();
 }
 
