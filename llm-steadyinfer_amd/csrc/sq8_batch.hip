@@ -73,7 +73,8 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void paged_attention_kernel(
   constexpr int W = kAttnWaves;
   __shared__ float s_m[W], s_l[W];
   __shared__ float s_acc[W][HS_MAX];
-  const int r = blockIdx.x / head_num, head = blockIdx.x % head_num;
+  const int id = xcd_grouped_id(head_num / kv_head_num);
+  const int r = id / head_num, head = id % head_num;
   const int seq = positions[r] + 1;
   const int kv_dim = kv_head_num * head_size;
   const int hoff = (head * kv_head_num / head_num) * head_size;

@@ -25,6 +25,18 @@ hipError_t launch_gemv_swiglu(const float* ab, const int8_t* w, const float* s, 
 hipError_t launch_generic(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
                           int K, int gs, hipStream_t st);
 
+// MI355X hands workgroups to its 8 XCDs round robin (workgroup b runs on XCD b % 8), and each
+// XCD has its own L2. This maps the hardware workgroup id to a logical one such that the logical
+// ids of each aligned group of G (query heads that read one kv head) run on one XCD at nearly the
+// same time, while successive groups still go round robin over the XCDs (load stays balanced).
+// A bijection when the grid is a multiple of 8 * G; identity otherwise.
+__device__ __forceinline__ int xcd_grouped_id(int G) {
+  const int b = blockIdx.x, n = gridDim.x;
+  if (G <= 1 || n % (8 * G) != 0) return b;
+  const int x = b & 7, s = b >> 3;
+  return ((s / G) * 8 + x) * G + s % G;
+}
+
 // Sign-extend byte `b` (0..3) of a dword and convert to fp32; exact for int8.
 __device__ __forceinline__ float byte_to_f32(uint32_t d, int b) {
   return static_cast<float>(static_cast<int32_t>(d << (24 - 8 * b)) >> 24);

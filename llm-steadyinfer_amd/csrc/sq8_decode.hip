@@ -247,7 +247,7 @@ __global__ __launch_bounds__(kAttnBlock) void attention_decode_kernel(
   __shared__ float s_v[HS_MAX];
   __shared__ float s_m[W], s_l[W];
   __shared__ float s_acc[W][HS_MAX];
-  const int head = blockIdx.x;
+  const int head = xcd_grouped_id(head_num / kv_head_num);
   const int pos = *pos_ptr;
   const int seq = pos + 1;
   const int kv_dim = kv_head_num * head_size;
