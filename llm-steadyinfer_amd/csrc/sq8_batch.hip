@@ -12,7 +12,15 @@ namespace sq8 {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kAttnWaves = 8;  // waves per (row, head) attention workgroup
+#ifndef SQ8_ATTN_WAVES
+#define SQ8_ATTN_WAVES 8
+#endif
+#ifndef SQ8_ATTN_CHUNK
+#define SQ8_ATTN_CHUNK 4
+#endif
+constexpr int kAttnWaves = SQ8_ATTN_WAVES;  // waves per (row, head) attention workgroup
+constexpr int kAttnChunk = SQ8_ATTN_CHUNK;  // cache positions per wave per load step
+constexpr int kRowU = 2;                   // positions per 16-lane group per step
 
 hipStream_t stream_of(void* s) { return static_cast<hipStream_t>(s); }
 int launched() { return hipGetLastError() == hipSuccess ? SQ8_OK : SQ8_ERR_LAUNCH; }
@@ -60,16 +68,19 @@ __global__ __launch_bounds__(kBlock) void paged_rope_kv_kernel(
 
 // One workgroup (kAttnWaves waves) per (row, query head); the decode attention design with the
 // cache rows addressed through the row's block table: wave w owns positions w, w + W, ...; lane l
-// holds head dims l, l + 64, ...; scores are wave-reduced dot products and the softmax runs online
-// per wave (running max, sum and weighted values), combined across the waves at the end.
-template <int HS_MAX>
+// holds DPL head dims (contiguous, one vector load per cache row, when VEC; else l, l + 64, ...);
+// scores are wave-reduced dot products and the softmax runs online per wave (running max, sum
+// and weighted values), combined across the waves at the end. kAttnChunk positions per wave are
+// loaded per step, and the next step's are in flight while one is used: a row's cache is read
+// at memory latency / (waves x chunk) positions, the bound when few rows are long.
+template <int HS_MAX, bool VEC>
 __global__ __launch_bounds__(kAttnWaves * kWave) void paged_attention_kernel(
     const float* __restrict__ qkv, int q_stride, int head_num, int kv_head_num, int head_size,
     const int32_t* __restrict__ positions, const int32_t* __restrict__ block_table,
     int table_stride, int block_size, const float* kcache, const float* vcache,
     float* __restrict__ out) {
   constexpr int DPL = HS_MAX / kWave;
-  constexpr int PCH = 4;
+  constexpr int PCH = kAttnChunk;
   constexpr int W = kAttnWaves;
   __shared__ float s_m[W], s_l[W];
   __shared__ float s_acc[W][HS_MAX];
@@ -83,20 +94,45 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void paged_attention_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nmine = wave < seq ? (seq - 1 - wave) / W + 1 : 0;
   const int nch = (nmine + PCH - 1) / PCH;
+  // Head dim j of this lane, and the first dim it loads (clamped into the head: lanes past
+  // head_size load valid elements and are never used).
+  auto dim = [&](int j) __attribute__((always_inline)) {
+    return VEC ? DPL * lane + j : lane + j * kWave;
+  };
+  const int d0 = VEC ? min(DPL * lane, head_size - DPL) : 0;
 
   float kr[2][PCH][DPL], vr[2][PCH][DPL];
-  // Branch-free: positions past the wave's last (and dims past head_size) re-read valid elements
-  // and are never used.
+  // Branch-free: positions past the wave's last re-read valid elements and are never used.
   auto load = [&](int b, int c) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < PCH; ++i) {
       const int t = min(wave + (c * PCH + i) * W, seq - 1);
       const size_t base = paged_row(table, t, block_size, kv_dim) + hoff;
+      if constexpr (VEC && DPL == 2) {
+        const float2 k2 = *reinterpret_cast<const float2*>(kcache + base + d0);
+        const float2 v2 = *reinterpret_cast<const float2*>(vcache + base + d0);
+        kr[b][i][0] = k2.x;
+        kr[b][i][1] = k2.y;
+        vr[b][i][0] = v2.x;
+        vr[b][i][1] = v2.y;
+      } else if constexpr (VEC && DPL == 4) {
+        const float4 k4 = *reinterpret_cast<const float4*>(kcache + base + d0);
+        const float4 v4 = *reinterpret_cast<const float4*>(vcache + base + d0);
+        kr[b][i][0] = k4.x;
+        kr[b][i][1] = k4.y;
+        kr[b][i][2] = k4.z;
+        kr[b][i][3] = k4.w;
+        vr[b][i][0] = v4.x;
+        vr[b][i][1] = v4.y;
+        vr[b][i][2] = v4.z;
+        vr[b][i][3] = v4.w;
+      } else {
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        const int d = min(lane + j * kWave, head_size - 1);
-        kr[b][i][j] = kcache[base + d];
-        vr[b][i][j] = vcache[base + d];
+        for (int j = 0; j < DPL; ++j) {
+          const int d = min(dim(j), head_size - 1);
+          kr[b][i][j] = kcache[base + d];
+          vr[b][i][j] = vcache[base + d];
+        }
       }
     }
   };
@@ -105,8 +141,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void paged_attention_kernel(
   const float* qrow = qkv + static_cast<size_t>(r) * q_stride + head * head_size;
   float qv[DPL];
 #pragma unroll
-  for (int j = 0; j < DPL; ++j)
-    qv[j] = lane + j * kWave < head_size ? qrow[lane + j * kWave] : 0.f;
+  for (int j = 0; j < DPL; ++j) qv[j] = dim(j) < head_size ? qrow[dim(j)] : 0.f;
   const float scale = 1.f / sqrtf(static_cast<float>(head_size));
   float m = -INFINITY, l = 0.f, acc[DPL];
 #pragma unroll
@@ -151,7 +186,7 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void paged_attention_kernel(
   }
 #pragma unroll
   for (int j = 0; j < DPL; ++j)
-    if (lane + j * kWave < head_size) s_acc[wave][lane + j * kWave] = acc[j];
+    if (dim(j) < head_size) s_acc[wave][dim(j)] = acc[j];
   __syncthreads();
   float mx = s_m[0];
 #pragma unroll
@@ -166,6 +201,170 @@ __global__ __launch_bounds__(kAttnWaves * kWave) void paged_attention_kernel(
       lt = fmaf(s_l[w], f, lt);
     }
     orow[d] = o / lt;
+  }
+}
+
+// Sum of v over the 16 lanes of each DPP row (lanes 16k .. 16k+15); every lane gets the sum.
+// quad_perm [1,0,3,2] and [2,3,0,1] sum each quad, row_half_mirror adds the other quad of the
+// half-row and row_mirror the other half: all VALU, no LDS permute.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  return v;
+}
+
+// One workgroup (W waves) per (row, kv head), for the G query heads that read the kv
+// head. Each 16-lane group of a wave owns one cache position at a time and lane li of the group
+// holds head dims DPL*li .. +DPL-1 (one coalesced 16*DPL-float row per group and load); a wave
+// steps over kRowStep positions (kRowU per group), the next step's rows in flight while one is
+// used. A score is a 16-lane DPP sum; the running max is updated once per step and head (the
+// wave's maximum over the step), so each (position, head) costs DPL FMAs, 4 DPP adds and one
+// exponential. Groups accumulate their own positions' weighted values under the wave's common
+// running max; groups, then waves, are combined at the end.
+template <int DPL, int GMAX, int W>
+__global__ __launch_bounds__(W * kWave) void paged_attention_rows_kernel(
+    const float* __restrict__ qkv, int q_stride, int head_num, int kv_head_num, int head_size,
+    const int32_t* __restrict__ positions, const int32_t* __restrict__ block_table,
+    int table_stride, int block_size, const float* kcache, const float* vcache,
+    float* __restrict__ out) {
+  constexpr int U = kRowU;
+  constexpr int SP = 4 * U;  // positions per wave per step
+  constexpr int HS = 16 * DPL;
+  constexpr int NV = DPL / 4;  // float4 per lane per cache row
+  __shared__ float s_m[W][GMAX], s_l[W][GMAX];
+  __shared__ float s_acc[W][GMAX][HS];
+  const int G = head_num / kv_head_num;
+  const int r = blockIdx.x / kv_head_num, kvh = blockIdx.x % kv_head_num;
+  const int seq = positions[r] + 1;
+  const int kv_dim = kv_head_num * HS, hoff = kvh * HS;
+  const int32_t* table = block_table + static_cast<size_t>(r) * table_stride;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = lane >> 4, li = lane & 15;
+  const int nsteps = (seq + SP - 1) / SP;
+  const int nmine = wave < nsteps ? (nsteps - 1 - wave) / W + 1 : 0;
+
+  float4 kb[2][U][NV], vb[2][U][NV];
+  // Position of group grp's u-th row at the wave's c-th step (re-reads position seq - 1 past the
+  // end; such scores are masked).
+  auto posn = [&](int c, int u) __attribute__((always_inline)) {
+    return (c * W + wave) * SP + u * 4 + grp;
+  };
+  auto load = [&](int b, int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const size_t base =
+          paged_row(table, min(posn(c, u), seq - 1), block_size, kv_dim) + hoff + DPL * li;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        kb[b][u][i] = *reinterpret_cast<const float4*>(kcache + base + 4 * i);
+        vb[b][u][i] = *reinterpret_cast<const float4*>(vcache + base + 4 * i);
+      }
+    }
+  };
+  if (nmine > 0) load(0, 0);
+
+  const float scale = 1.f / sqrtf(static_cast<float>(HS));
+  const float* qrow = qkv + static_cast<size_t>(r) * q_stride + kvh * G * HS + DPL * li;
+  float q[GMAX][DPL], m[GMAX], l[GMAX], acc[GMAX][DPL];
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      q[g][j] = g < G ? qrow[g * HS + j] * scale : 0.f;
+      acc[g][j] = 0.f;
+    }
+  }
+  auto step = [&](int b, int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int g = 0; g < GMAX; ++g) {
+      if (g >= G) break;
+      float s[U], mx = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          a = fmaf(q[g][4 * i], kb[b][u][i].x, a);
+          a = fmaf(q[g][4 * i + 1], kb[b][u][i].y, a);
+          a = fmaf(q[g][4 * i + 2], kb[b][u][i].z, a);
+          a = fmaf(q[g][4 * i + 3], kb[b][u][i].w, a);
+        }
+        const float sum = row16_sum(a);  // all lanes of the row take part
+        s[u] = posn(c, u) < seq ? sum : -INFINITY;
+        mx = fmaxf(mx, s[u]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      const float mn = fmaxf(m[g], mx);  // finite: the step's first position is < seq
+      const float f = expf(m[g] - mn);
+      l[g] *= f;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) acc[g][j] *= f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float p = expf(s[u] - mn);
+        l[g] += p;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          acc[g][4 * i] = fmaf(p, vb[b][u][i].x, acc[g][4 * i]);
+          acc[g][4 * i + 1] = fmaf(p, vb[b][u][i].y, acc[g][4 * i + 1]);
+          acc[g][4 * i + 2] = fmaf(p, vb[b][u][i].z, acc[g][4 * i + 2]);
+          acc[g][4 * i + 3] = fmaf(p, vb[b][u][i].w, acc[g][4 * i + 3]);
+        }
+      }
+      m[g] = mn;
+    }
+  };
+  for (int c = 0; c < nmine; c += 2) {
+    load(1, min(c + 1, nmine - 1));
+    step(0, c);
+    if (c + 1 >= nmine) break;
+    load(0, min(c + 2, nmine - 1));
+    step(1, c + 1);
+  }
+
+  // Sum the 4 groups (same running max), then combine the waves.
+#pragma unroll
+  for (int g = 0; g < GMAX; ++g) {
+    if (g >= G) break;
+    float lt = l[g];
+    lt += __shfl_xor(lt, 16, kWave);
+    lt += __shfl_xor(lt, 32, kWave);
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      float a = acc[g][j];
+      a += __shfl_xor(a, 16, kWave);
+      a += __shfl_xor(a, 32, kWave);
+      acc[g][j] = a;
+    }
+    if (lane == 0) {
+      s_m[wave][g] = m[g];
+      s_l[wave][g] = lt;
+    }
+    if (grp == 0) {
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) s_acc[wave][g][DPL * li + j] = acc[g][j];
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < G * HS; e += W * kWave) {
+    const int g = e / HS, d = e % HS;
+    float mx = s_m[0][g];
+#pragma unroll
+    for (int w = 1; w < W; ++w) mx = fmaxf(mx, s_m[w][g]);
+    float o = 0.f, lt = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float f = s_m[w][g] == -INFINITY ? 0.f : expf(s_m[w][g] - mx);
+      o = fmaf(s_acc[w][g][d], f, o);
+      lt = fmaf(s_l[w][g], f, lt);
+    }
+    out[(static_cast<size_t>(r) * head_num + kvh * G + g) * HS + d] = o / lt;
   }
 }
 
@@ -271,15 +470,43 @@ int sq8_paged_attention(const float* qkv, int q_stride, int rows, int head_num, 
       head_size <= 0 || head_size > 256 || q_stride < head_num * head_size || table_stride <= 0 ||
       block_size <= 0 || static_cast<int64_t>(rows) * head_num > 0x7fffffff)
     return SQ8_ERR_DIMS;
+  const hipStream_t st = stream_of(hip_stream);
+  const int G = head_num / kv_head_num;
+  const bool k16 = reinterpret_cast<uintptr_t>(key_cache) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(value_cache) % 16 == 0;
+  if ((head_size == 128 || head_size == 64) && G <= 8 && k16 &&
+      static_cast<int64_t>(rows) * kv_head_num <= 0x7fffffff) {
+    // Few workgroups (few, typically long, rows): 8 waves each to keep more rows in flight.
+    const bool wide = static_cast<int64_t>(rows) * kv_head_num < 2 * cu_count();
+    const dim3 grid(rows * kv_head_num), block((wide ? 8 : 4) * kWave);
+    const auto rk = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, grid, block, 0, st, qkv, q_stride, head_num, kv_head_num,
+                         head_size, positions, block_table, table_stride, block_size, key_cache,
+                         value_cache, out);
+    };
+    if (head_size == 64)
+      wide ? rk(paged_attention_rows_kernel<4, 8, 8>) : rk(paged_attention_rows_kernel<4, 8, 4>);
+    else if (G <= 4)
+      wide ? rk(paged_attention_rows_kernel<8, 4, 8>) : rk(paged_attention_rows_kernel<8, 4, 4>);
+    else
+      wide ? rk(paged_attention_rows_kernel<8, 8, 8>) : rk(paged_attention_rows_kernel<8, 8, 4>);
+    return launched();
+  }
   const dim3 grid(rows * head_num), block(kAttnWaves * kWave);
+  // One vector load per cache row when every lane's dims are contiguous and aligned.
+  const int dpl = head_size <= 128 ? 2 : 4;
+  const bool vec = head_size % dpl == 0 && kv_head_num * head_size % dpl == 0 &&
+                   reinterpret_cast<uintptr_t>(key_cache) % (4 * dpl) == 0 &&
+                   reinterpret_cast<uintptr_t>(value_cache) % (4 * dpl) == 0;
+  const auto args = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, block, 0, st, qkv, q_stride, head_num, kv_head_num, head_size,
+                       positions, block_table, table_stride, block_size, key_cache, value_cache,
+                       out);
+  };
   if (head_size <= 128)
-    hipLaunchKernelGGL((paged_attention_kernel<128>), grid, block, 0, stream_of(hip_stream), qkv,
-                       q_stride, head_num, kv_head_num, head_size, positions, block_table,
-                       table_stride, block_size, key_cache, value_cache, out);
+    vec ? args(paged_attention_kernel<128, true>) : args(paged_attention_kernel<128, false>);
   else
-    hipLaunchKernelGGL((paged_attention_kernel<256>), grid, block, 0, stream_of(hip_stream), qkv,
-                       q_stride, head_num, kv_head_num, head_size, positions, block_table,
-                       table_stride, block_size, key_cache, value_cache, out);
+    vec ? args(paged_attention_kernel<256, true>) : args(paged_attention_kernel<256, false>);
   return launched();
 }
 
