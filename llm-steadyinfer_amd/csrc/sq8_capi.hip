@@ -20,10 +20,12 @@ bool fast_shape(int K, int gs) { return gs % 16 == 0 && K % gs == 0; }
 // Up to 4 token rows whose activations fit the LDS budget go to the VALU GEMV (measured faster
 // than the matrix-core kernels there); everything else with 64-wide groups to the MFMA path.
 Path choose(int M, int N, int K, int gs, bool aligned) {
-  (void)N;
   if (!aligned || !fast_shape(K, gs)) return Path::kGeneric;
   if (sq8::gemv_stream_fits(M, K)) return Path::kGemv;
-  if (M >= 3 && gs % 64 == 0) return Path::kMfma;
+  // The MFMA kernels address weights, scales and activations with 32-bit byte offsets.
+  const bool off32 = static_cast<int64_t>(N) * K < (int64_t{1} << 31) &&
+                     static_cast<int64_t>(M) * K * 4 < (int64_t{1} << 31);
+  if (M >= 3 && gs % 64 == 0 && off32) return Path::kMfma;
   return Path::kGemv;
 }
 

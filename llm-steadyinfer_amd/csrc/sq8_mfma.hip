@@ -14,9 +14,9 @@
 //  * One K step of the main loop is one 64-wide weight group. Its partial product P (hi and lo
 //    MFMAs chained in fp32) is formed from zero, then acc += scale[n, g] * P with one FMA per
 //    output: the per-group scale never touches the weights, so no rounding is added on that side.
-//  * v_mfma_f32_32x32x16_f16 tiles; a 256-thread workgroup (4 waves) owns a BM x BN output tile;
-//    the next group's activations and weights are loaded into registers while the current group is
-//    multiplied from LDS (double-buffered LDS, one barrier per group).
+//  * v_mfma_f32_32x32x16_f16 tiles; a workgroup of 4 or 8 waves owns a 64 x 256 or 128 x 256
+//    output tile and streams its operands through a 3-deep ring of LDS stages filled by direct
+//    global -> LDS DMA (gemm_kernel below), one barrier per group.
 //  * Skinny shapes (few tokens, few output tiles) split K over gridDim.z; partial tiles go to the
 //    workspace and a second kernel sums them in split order (deterministic).
 #include <algorithm>
@@ -91,99 +91,132 @@ __device__ __forceinline__ void i8x4_to_h4(uint32_t d, uint32_t& lo, uint32_t& h
   hi = __builtin_bit_cast(uint32_t, hb);
 }
 
-// ---------------------------------------------------------------- main GEMM
-// Waves laid out WAVES_M x WAVES_N; each wave owns TM x TN tiles of 32 x 32.
-template <int WAVES_M, int WAVES_N, int TM, int TN>
-struct Tile {
-  static_assert(WAVES_M * WAVES_N == kThreads / kWave, "4 waves per workgroup");
+// ---------------------------------------------------------------- pipelined GEMM (LDS DMA)
+// Same arithmetic as mfma_gemm_kernel (hi/lo activation MFMAs per 64-wide group, acc += scale * P),
+// fed by a STAGES-deep ring of LDS stages that global_load_lds_dwordx4 fills straight from memory:
+// no register staging, so several groups of loads are in flight per wave while the MFMAs run.
+//  * Stage layout: x hi [BM][64] f16, x lo [BM][64] f16, w [BN][64] int8 (converted to f16 after
+//    the LDS read), scales [BN] fp32 (stored twice per 32 columns, see below).
+//  * A DMA instruction writes lane i's 16 bytes to LDS slot base + 16 * i, so the layout is chosen
+//    by which global chunk each lane fetches. Chunks are XOR-swizzled within a row so that the
+//    MFMA operand reads (32 rows x one 16-byte chunk per instruction) hit distinct banks:
+//    x row r keeps chunk c at slot c ^ fx(r), w row r keeps chunk q at slot q ^ fw(r).
+//  * The loads are issued from inline asm, so the compiler does not count them; every thread
+//    issues the same number per stage (LOADS), and before reading stage s a thread waits until at
+//    most (STAGES - 2) stages of its own loads are outstanding, then a barrier publishes all
+//    threads' loads. The same barrier tells every wave that the stage being refilled next has
+//    been read by all waves. One barrier per 64-wide group.
+__device__ __forceinline__ int swz_x(int r) { return (r ^ (r >> 3)) & 7; }
+__device__ __forceinline__ int swz_w(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+
+// One 16-byte global -> LDS copy per lane: lane i writes LDS [lds_base + 16 i]. m0 (the LDS
+// base register of the DMA) is saved and restored around the copy.
+__device__ __forceinline__ void dma16(const void* base, uint32_t voff, uint32_t lds_base) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, %3\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_base), "v"(voff), "s"(base)
+      : "memory");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t voff, uint32_t lds_base) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dword %2, %3\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_base), "v"(voff), "s"(base)
+      : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  // gfx9 s_waitcnt encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int WAVES_M, int WAVES_N, int TM, int TN, int STAGES>
+struct PTile {
+  static constexpr int NW = WAVES_M * WAVES_N;
+  static constexpr int NT = NW * kWave;
   static constexpr int BM = WAVES_M * TM * 32;
   static constexpr int BN = WAVES_N * TN * 32;
-  static constexpr int XCH = BM * 8 / kThreads;   // 16-byte x chunks per thread per stage (hi or lo)
-  static constexpr int WCH = BN * 4 / kThreads;   // 16-byte weight chunks per thread per stage
-  static_assert(XCH >= 1 && WCH >= 1, "tile too small for the staging pattern");
-  static constexpr int STAGE_HALVES = (2 * BM + BN) * LDS_STRIDE;
-  static constexpr size_t LDS_BYTES = 2ull * STAGE_HALVES * sizeof(_Float16);
+  static constexpr int XB = BM * 128;            // bytes of x hi (or lo) per stage
+  static constexpr int WB = BN * 64;             // bytes of int8 weights per stage
+  static constexpr int SB = BN * 8;              // scale bytes per stage (each 32-column run twice)
+  static constexpr int STAGE = 2 * XB + WB + SB;
+  static constexpr size_t LDS_BYTES = static_cast<size_t>(STAGES) * STAGE;
+  static constexpr int XL = BM * 8 / NT;         // x DMA instructions per thread per stage (hi or lo)
+  static constexpr int WL = BN * 4 / NT;         // weight DMA instructions per thread per stage
+  static constexpr int SL = BN / 32 / NW;        // scale DMA instructions per thread per stage
+  static constexpr int LOADS = 2 * XL + WL + SL;
+  static_assert(XL >= 1 && WL >= 1 && SL >= 1 && BM * 8 % NT == 0 && BN * 4 % NT == 0 &&
+                    (BN / 32) % NW == 0,
+                "tile does not match the DMA pattern");
+  static_assert((STAGES - 2) * LOADS < 64, "vmcnt range");
+  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 };
 
-template <int WAVES_M, int WAVES_N, int TM, int TN>
-__global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
+template <int WAVES_M, int WAVES_N, int TM, int TN, int STAGES>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
     const _Float16* xh, const _Float16* xl, const float* __restrict__ rscale, const int8_t* w,
     const float* s, float* __restrict__ out, int M, int N, int K, int gs, int groups_per_split) {
-  using T = Tile<WAVES_M, WAVES_N, TM, TN>;
-  extern __shared__ _Float16 lds[];
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
+  using T = PTile<WAVES_M, WAVES_N, TM, TN, STAGES>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int n0 = blockIdx.x * T::BN, m0 = blockIdx.y * T::BM;
   const int nsteps = K / BK;
   const int st_begin = blockIdx.z * groups_per_split;
   const int st_end = min(nsteps, st_begin + groups_per_split);
   const int gpr = K / gs;
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
 
-  // Staging assignment (fixed per thread).
-  const _Float16* xh_src[T::XCH];
-  const _Float16* xl_src[T::XCH];
-  int x_dst[T::XCH];
+  // Per-thread DMA sources (byte offsets; the K offset of a stage is added to the base pointer).
+  uint32_t xoff[T::XL], woff[T::WL], soff[T::SL];
 #pragma unroll
-  for (int i = 0; i < T::XCH; ++i) {
-    const int c = tid + kThreads * i, row = c >> 3, part = c & 7;
-    const int m = min(m0 + row, M - 1);
-    xh_src[i] = xh + static_cast<size_t>(m) * K + part * 8;
-    xl_src[i] = xl + static_cast<size_t>(m) * K + part * 8;
-    x_dst[i] = row * LDS_STRIDE + part * 8;
+  for (int i = 0; i < T::XL; ++i) {
+    const int slot = (i * T::NW + wave) * kWave + lane;
+    const int r = slot >> 3, c = (slot & 7) ^ swz_x(slot >> 3);
+    xoff[i] = static_cast<uint32_t>(min(m0 + r, M - 1)) * K * 2u + c * 16u;
   }
-  const int8_t* w_src[T::WCH];
-  int w_dst[T::WCH];
 #pragma unroll
-  for (int i = 0; i < T::WCH; ++i) {
-    const int c = tid + kThreads * i, row = c >> 2, part = c & 3;
-    const int n = min(n0 + row, N - 1);
-    w_src[i] = w + static_cast<size_t>(n) * K + part * 16;
-    w_dst[i] = row * LDS_STRIDE + part * 16;
+  for (int i = 0; i < T::WL; ++i) {
+    const int slot = (i * T::NW + wave) * kWave + lane;
+    const int r = slot >> 2, q = (slot & 3) ^ swz_w(slot >> 2);
+    woff[i] = static_cast<uint32_t>(min(n0 + r, N - 1)) * K + q * 16u;
   }
-  // Scale pointers for this lane's output columns.
-  const float* s_src[TN];
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    const int n = min(n0 + (wn * TN + j) * 32 + (lane & 31), N - 1);
-    s_src[j] = s + static_cast<size_t>(n) * gpr;
+  for (int i = 0; i < T::SL; ++i) {
+    const int run = i * T::NW + wave;            // 32-column run of this instruction
+    const int c = run * 32 + (lane & 31);
+    soff[i] = static_cast<uint32_t>(min(n0 + c, N - 1)) * gpr * 4u;
   }
-
-  u32x4 rxh[T::XCH], rxl[T::XCH], rw[T::WCH];
-  float rs[TN];
-  auto gload = [&](int st) __attribute__((always_inline)) {
-    const int k0 = st * BK;
+  auto issue = [&](int st, int buf) __attribute__((always_inline)) {
+    const uint32_t sb = lds0 + buf * T::STAGE;
+    const char* xhb = reinterpret_cast<const char*>(xh) + static_cast<size_t>(st) * BK * 2;
+    const char* xlb = reinterpret_cast<const char*>(xl) + static_cast<size_t>(st) * BK * 2;
+    const char* wb = reinterpret_cast<const char*>(w) + static_cast<size_t>(st) * BK;
+    const char* sbp = reinterpret_cast<const char*>(s) + static_cast<size_t>(st * BK / gs) * 4;
 #pragma unroll
-    for (int i = 0; i < T::XCH; ++i) {
-      rxh[i] = *reinterpret_cast<const u32x4*>(xh_src[i] + k0);
-      rxl[i] = *reinterpret_cast<const u32x4*>(xl_src[i] + k0);
+    for (int i = 0; i < T::XL; ++i) {
+      const uint32_t d = ((i * T::NW + wave) * kWave) * 16;
+      dma16(xhb, xoff[i], sb + d);
+      dma16(xlb, xoff[i], sb + T::XB + d);
     }
 #pragma unroll
-    for (int i = 0; i < T::WCH; ++i)
-      rw[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w_src[i] + k0));
+    for (int i = 0; i < T::WL; ++i)
+      dma16(wb, woff[i], sb + 2 * T::XB + ((i * T::NW + wave) * kWave) * 16);
 #pragma unroll
-    for (int j = 0; j < TN; ++j) rs[j] = s_src[j][k0 / gs];
-  };
-  auto lstore = [&](int buf) __attribute__((always_inline)) {
-    _Float16* sxh = lds + buf * T::STAGE_HALVES;
-    _Float16* sxl = sxh + T::BM * LDS_STRIDE;
-    _Float16* sw = sxl + T::BM * LDS_STRIDE;
-#pragma unroll
-    for (int i = 0; i < T::XCH; ++i) {
-      *reinterpret_cast<u32x4*>(sxh + x_dst[i]) = rxh[i];
-      *reinterpret_cast<u32x4*>(sxl + x_dst[i]) = rxl[i];
-    }
-#pragma unroll
-    for (int i = 0; i < T::WCH; ++i) {
-      uint32_t h[8];
-      i8x4_to_h4(rw[i].x, h[0], h[1]);
-      i8x4_to_h4(rw[i].y, h[2], h[3]);
-      i8x4_to_h4(rw[i].z, h[4], h[5]);
-      i8x4_to_h4(rw[i].w, h[6], h[7]);
-      const u32x4 a = {h[0], h[1], h[2], h[3]};
-      const u32x4 b = {h[4], h[5], h[6], h[7]};
-      *reinterpret_cast<u32x4*>(sw + w_dst[i]) = a;
-      *reinterpret_cast<u32x4*>(sw + w_dst[i] + 8) = b;
-    }
+    for (int i = 0; i < T::SL; ++i)
+      dma4(sbp, soff[i], sb + 2 * T::XB + T::WB + (i * T::NW + wave) * 256);
   };
 
   f16v acc[TM][TN];
@@ -194,44 +227,59 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // Lane's operand rows/columns inside the stage and its 32-wide K half.
-  const int lrow = lane & 31, khalf = (lane >> 5) * 32;
-  float cur_s[TN];
-  if (st_begin < st_end) {
-    gload(st_begin);
-    lstore(0);
+  // Lane's LDS read offsets inside a stage.
+  const int lrow = lane & 31, half = lane >> 5;
+  int aoff[TM], boff[TN], scoff[TN];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) cur_s[j] = rs[j];
+  for (int i = 0; i < TM; ++i) {
+    const int r = (wm * TM + i) * 32 + lrow;
+    aoff[i] = r * 128 + ((half * 4) ^ swz_x(r)) * 16;   // chunk t of the lane: aoff ^ (16 t)
   }
-  __syncthreads();
-  // Branch-free steps: the prefetch and the store of the next stage are unconditional (past the
-  // end they repeat the last step into the stage that is not read again). A load issued on only
-  // one branch makes the compiler's wait counts assume the other branch, so the first use of this
-  // step's data would also wait for the whole prefetch.
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int r = (wn * TN + j) * 32 + lrow;
+    boff[j] = 2 * T::XB + r * 64 + ((half * 2) ^ swz_w(r)) * 16;  // chunk 2h+u: boff ^ (16 u)
+    scoff[j] = 2 * T::XB + T::WB + (r >> 5) * 256 + (r & 31) * 4;
+  }
+
+  if (st_begin < st_end) {
+#pragma unroll
+    for (int p = 0; p < STAGES - 1; ++p) issue(min(st_begin + p, st_end - 1), p);
+  }
   for (int st = st_begin; st < st_end; ++st) {
-    const int buf = (st - st_begin) & 1;
-    asm volatile("" ::: "memory");
-    gload(min(st + 1, st_end - 1));
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    const _Float16* sxh = lds + buf * T::STAGE_HALVES;
-    const _Float16* sxl = sxh + T::BM * LDS_STRIDE;
-    const _Float16* sw = sxl + T::BM * LDS_STRIDE;
+    const int rel = st - st_begin;
+    wait_vmcnt<(STAGES - 2) * T::LOADS>();
+    __syncthreads();
+    issue(min(st + STAGES - 1, st_end - 1), (rel + STAGES - 1) % STAGES);
+    const char* sp = smem + (rel % STAGES) * T::STAGE;
+    h8 bw[TN][4];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const u32x4 raw = *reinterpret_cast<const u32x4*>(sp + (boff[j] ^ (16 * u)));
+        uint32_t h[8];
+        i8x4_to_h4(raw.x, h[0], h[1]);
+        i8x4_to_h4(raw.y, h[2], h[3]);
+        i8x4_to_h4(raw.z, h[4], h[5]);
+        i8x4_to_h4(raw.w, h[6], h[7]);
+        const u32x4 a = {h[0], h[1], h[2], h[3]};
+        const u32x4 b = {h[4], h[5], h[6], h[7]};
+        bw[j][2 * u] = __builtin_bit_cast(h8, a);
+        bw[j][2 * u + 1] = __builtin_bit_cast(h8, b);
+      }
+    }
+    float sc[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) sc[j] = *reinterpret_cast<const float*>(sp + scoff[j]);
     f16v p[TM][TN];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int ko = khalf + 8 * t;
-      h8 ah[TM], al[TM], bw[TN];
+      h8 ah[TM], al[TM];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
-        const int row = (wm * TM + i) * 32 + lrow;
-        ah[i] = *reinterpret_cast<const h8*>(sxh + row * LDS_STRIDE + ko);
-        al[i] = *reinterpret_cast<const h8*>(sxl + row * LDS_STRIDE + ko);
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int col = (wn * TN + j) * 32 + lrow;
-        bw[j] = *reinterpret_cast<const h8*>(sw + col * LDS_STRIDE + ko);
+        ah[i] = *reinterpret_cast<const h8*>(sp + (aoff[i] ^ (16 * t)));
+        al[i] = *reinterpret_cast<const h8*>(sp + T::XB + (aoff[i] ^ (16 * t)));
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
@@ -239,11 +287,11 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
         for (int j = 0; j < TN; ++j) {
           if (t == 0) {
             const f16v zero = {};
-            p[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j], zero, 0, 0, 0);
+            p[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j][t], zero, 0, 0, 0);
           } else {
-            p[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j], p[i][j], 0, 0, 0);
+            p[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j][t], p[i][j], 0, 0, 0);
           }
-          p[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bw[j], p[i][j], 0, 0, 0);
+          p[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bw[j][t], p[i][j], 0, 0, 0);
         }
     }
 #pragma unroll
@@ -251,23 +299,17 @@ __global__ __launch_bounds__(kThreads) void mfma_gemm_kernel(
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(cur_s[j], p[i][j][r], acc[i][j][r]);
-    // Keep the next stage's conversion after the MFMAs: hoisted into them it would wait for the
-    // prefetch at the top of the step.
-    __builtin_amdgcn_sched_barrier(0);
-    lstore(buf ^ 1);
-#pragma unroll
-    for (int j = 0; j < TN; ++j) cur_s[j] = rs[j];
-    __syncthreads();
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(sc[j], p[i][j][r], acc[i][j][r]);
   }
+  // Drain the clamped tail loads before the workgroup's LDS is released.
+  wait_vmcnt<0>();
 
-  // Epilogue: undo the activation power of two and store (to y, or to this split's partial).
   float* dst = out + static_cast<size_t>(blockIdx.z) * M * N;
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int m = m0 + (wm * TM + i) * 32 + 8 * (r >> 2) + (lane >> 5) * 4 + (r & 3);
+      const int m = m0 + (wm * TM + i) * 32 + 8 * (r >> 2) + half * 4 + (r & 3);
       if (m >= M) continue;
       const float rsc = rscale[m];
 #pragma unroll
@@ -1057,7 +1099,7 @@ struct Plan {
   int rt, tn, tw; // tile: 16-row activation tiles, 16-column tiles per wave, waves per workgroup
   bool skinny;
   int kw;         // skinny: K groups per chunk (divides groups_per_split)
-  int cfg;        // GEMM: 0: 32x256 tile, 1: 64x128, 2: 128x128.  Skinny: 0: MT=1, 1: MT=2
+  int cfg;        // GEMM: 1: 64x256 tile, 2: 128x256.  Skinny: 0: MT=1, 1: MT=2
   int bm, bn;
   int splits;
   int groups_per_split;
@@ -1111,23 +1153,36 @@ Plan make_plan(int M, int N, int K) {
     p.splits = (chunks + cps - 1) / cps;
     return p;
   }
-  if (M <= 32) { p.cfg = 0; p.bm = 32; p.bn = 256; }
-  else if (M <= 64) { p.cfg = 1; p.bm = 64; p.bn = 128; }
-  else { p.cfg = 2; p.bm = 128; p.bn = 128; }
+  // Pipelined GEMM: one 64 x 256 (M <= 64) or 128 x 256 tile per workgroup, one workgroup per CU
+  // (its LDS ring takes ~100 or ~150 KiB). K is split when that evens out the rounds of
+  // workgroups over the CUs: cost = rounds / splits plus a small charge per split for the
+  // partial tiles and the reduction.
+  p.cfg = M <= 64 ? 1 : 2;
+  p.bm = M <= 64 ? 64 : 128;
+  p.bn = 256;
+  const int cus = cu_count();
   const int tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
   int splits = 1;
-  if (tiles < target) splits = min(min(16, nsteps), (target + tiles - 1) / tiles);
+  double best = 1e30;
+  // The 64-row tile streams weights (partials are cheap next to them); the 128-row tile is
+  // MFMA-bound and pays more for its partials.
+  const double charge = p.cfg == 1 ? 0.005 : 0.04;
+  for (int sp = 1; sp <= 16 && sp * 4 <= nsteps; ++sp) {
+    const double rounds = static_cast<double>((tiles * sp + cus - 1) / cus);
+    const double cost = rounds / sp + charge * (sp - 1);
+    if (cost < best - 1e-9) { best = cost; splits = sp; }
+  }
   p.groups_per_split = (nsteps + splits - 1) / splits;
   p.splits = (nsteps + p.groups_per_split - 1) / p.groups_per_split;
   return p;
 }
 
-template <int WM, int WN, int TM, int TN>
-hipError_t launch_gemm(const _Float16* xh, const _Float16* xl, const float* rsc, const int8_t* w,
-                       const float* s, float* out, int M, int N, int K, int gs, const Plan& p,
-                       hipStream_t st) {
-  using T = Tile<WM, WN, TM, TN>;
-  auto kern = mfma_gemm_kernel<WM, WN, TM, TN>;
+template <int WM, int WN, int TM, int TN, int STAGES>
+hipError_t launch_gemm(const _Float16* xh, const _Float16* xl, const float* rsc,
+                            const int8_t* w, const float* s, float* out, int M, int N, int K,
+                            int gs, const Plan& p, hipStream_t st) {
+  using T = PTile<WM, WN, TM, TN, STAGES>;
+  auto kern = gemm_kernel<WM, WN, TM, TN, STAGES>;
   static bool attr_set = false;  // LDS above 64 KiB needs the opt-in attribute
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -1137,7 +1192,7 @@ hipError_t launch_gemm(const _Float16* xh, const _Float16* xl, const float* rsc,
     attr_set = true;
   }
   const dim3 grid((N + T::BN - 1) / T::BN, (M + T::BM - 1) / T::BM, p.splits);
-  hipLaunchKernelGGL(kern, grid, dim3(kThreads), T::LDS_BYTES, st, xh, xl, rsc, w, s, out, M, N, K,
+  hipLaunchKernelGGL(kern, grid, dim3(T::NT), T::LDS_BYTES, st, xh, xl, rsc, w, s, out, M, N, K,
                      gs, p.groups_per_split);
   return hipGetLastError();
 }
@@ -1268,11 +1323,10 @@ hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y
   hipLaunchKernelGGL(split_x_kernel, dim3(M), dim3(kThreads), 0, st, x, xh, xl, rsc, K);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  switch (p.cfg) {
-    case 0: e = launch_gemm<1, 4, 1, 2>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st); break;
-    case 1: e = launch_gemm<2, 2, 1, 2>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st); break;
-    default: e = launch_gemm<2, 2, 2, 2>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st); break;
-  }
+  if (p.cfg == 1)
+    e = launch_gemm<1, 4, 2, 2, 3>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st);
+  else
+    e = launch_gemm<2, 4, 2, 2, 3>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st);
   if (e != hipSuccess || p.splits == 1) return e;
   const size_t count = static_cast<size_t>(M) * N;
   const int grid = static_cast<int>(std::min<size_t>((count + kThreads - 1) / kThreads, 4096));
