@@ -53,6 +53,34 @@ int sq8_matmul(const float* x, const int8_t* w, const float* scales, float* y, i
  * split-K partials here. */
 size_t sq8_workspace_bytes(int M, int N, int K, int group_size);
 
+/* Output epilogues of sq8_matmul_epilogue. */
+enum sq8_epilogue {
+  SQ8_EPI_NONE = 0,      /* y[M][N] = x . W^T (as sq8_matmul) */
+  SQ8_EPI_RESIDUAL = 1,  /* y[M][N] = residual[M][N] + x . W^T; residual may be y itself */
+  SQ8_EPI_SWIGLU = 2     /* W is the fused gate/up weight [w1; w3] (N = 2F rows, the F gate rows
+                            first, each row's scales with it); y[M][F] = silu(g) * u with
+                            g = x . w1^T, u = x . w3^T, silu(g) = g / (1 + e^-g) */
+};
+
+/* y = epilogue(x . W^T) in one pass over the weights where the kernel fuses it. Replaces the
+ * separate operators that follow the projections in the reference's batched forward
+ * (src/source/model/llama3.cpp:1139-1179): the residual adds after wo and w2
+ * (AddLayer, add_kernel.cu) and the SwiGLU of w1/w3 (swiglu_kernel.cu); the reference keeps w1
+ * and w3 separate, here they are one fused weight. The prefill GEMM (token counts where
+ * sq8_epilogue_fused() is 1) applies the epilogue in its output stage (or in its split-K
+ * reduction); other paths run the product into the workspace and apply the epilogue in one
+ * elementwise launch. Arguments and errors as sq8_matmul; SQ8_ERR_DIMS if SwiGLU has an odd N,
+ * SQ8_ERR_NULL if the residual epilogue has no residual. */
+int sq8_matmul_epilogue(const float* x, const int8_t* w, const float* scales, float* y, int M,
+                        int N, int K, int group_size, int epilogue, const float* residual,
+                        void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/* Workspace bytes of sq8_matmul_epilogue (includes the product buffer of unfused paths). */
+size_t sq8_epilogue_workspace_bytes(int M, int N, int K, int group_size, int epilogue);
+
+/* 1 if sq8_matmul_epilogue fuses the epilogue into the matmul kernel for this shape, else 0. */
+int sq8_epilogue_fused(int M, int N, int K, int group_size);
+
 /* Human-readable text of a status code. */
 const char* sq8_status_string(int status);
 

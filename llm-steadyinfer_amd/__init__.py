@@ -21,7 +21,13 @@ SQ8_ERR_WORKSPACE = -4
 SQ8_ERR_LAUNCH = -5
 SQ8_ERR_DEVICE = -6
 
-EXPORTED_SYMBOLS = ("sq8_matmul", "sq8_workspace_bytes", "sq8_status_string", "sq8_path_name")
+EXPORTED_SYMBOLS = ("sq8_matmul", "sq8_workspace_bytes", "sq8_status_string", "sq8_path_name",
+                    "sq8_matmul_epilogue", "sq8_epilogue_workspace_bytes", "sq8_epilogue_fused")
+
+# Output epilogues (include/sq8.h, enum sq8_epilogue).
+SQ8_EPI_NONE = 0
+SQ8_EPI_RESIDUAL = 1
+SQ8_EPI_SWIGLU = 2
 # include/sq8_decode.h
 DECODE_SYMBOLS = ("sq8_embedding", "sq8_rmsnorm", "sq8_add_rmsnorm", "sq8_rope_tables", "sq8_rope_kv",
                   "sq8_attention_decode", "sq8_swiglu", "sq8_add", "sq8_argmax_workspace_bytes",
@@ -56,6 +62,12 @@ def lib() -> ctypes.CDLL:
         L.sq8_status_string.restype = ctypes.c_char_p
         L.sq8_path_name.argtypes = [I, I, I, I]
         L.sq8_path_name.restype = ctypes.c_char_p
+        L.sq8_matmul_epilogue.argtypes = [vp, vp, vp, vp, I, I, I, I, I, vp, vp, sz, vp]
+        L.sq8_matmul_epilogue.restype = I
+        L.sq8_epilogue_workspace_bytes.argtypes = [I, I, I, I, I]
+        L.sq8_epilogue_workspace_bytes.restype = sz
+        L.sq8_epilogue_fused.argtypes = [I, I, I, I]
+        L.sq8_epilogue_fused.restype = I
         f32 = ctypes.c_float
         sigs = {
             "sq8_embedding": [vp, I, I, vp, I, vp, vp],
@@ -150,6 +162,36 @@ def matmul(x, w, scales, y=None, group_size: int = 64, workspace: Workspace | No
     if rc != SQ8_OK:
         raise Sq8Error(rc)
     return y.reshape(-1) if squeeze else y
+
+
+def epilogue_fused(M: int, N: int, K: int, group_size: int = 64) -> bool:
+    return bool(lib().sq8_epilogue_fused(M, N, K, group_size))
+
+
+def matmul_epilogue(x, w, scales, y, epilogue: int, residual=None, group_size: int = 64,
+                    workspace: Workspace | None = None, stream=None):
+    """y = epilogue(x[M,K] @ dequant(w[N,K], scales).T) through sq8_matmul_epilogue.
+
+    SQ8_EPI_RESIDUAL: y[M,N] = residual + product (residual may be y itself).
+    SQ8_EPI_SWIGLU: w is the fused [w1; w3] (N = 2F); y[M,F] = silu(gate) * up."""
+    import torch
+    M, K = x.shape
+    N = w.shape[0]
+    for t in (x, w, scales, y) + ((residual,) if residual is not None else ()):
+        if not t.is_contiguous():
+            raise ValueError("sq8 tensors must be contiguous")
+    if stream is None:
+        stream = torch.cuda.current_stream(x.device)
+    if workspace is None:
+        workspace = _default_ws.setdefault(str(x.device), Workspace(x.device))
+    ws_ptr, ws_n = workspace.get(int(lib().sq8_epilogue_workspace_bytes(M, N, K, group_size,
+                                                                         epilogue)))
+    rc = int(lib().sq8_matmul_epilogue(x.data_ptr(), w.data_ptr(), scales.data_ptr(),
+                                       y.data_ptr(), M, N, K, group_size, epilogue,
+                                       _ptr(residual), ws_ptr or None, ws_n, stream.cuda_stream))
+    if rc != SQ8_OK:
+        raise Sq8Error(rc)
+    return y
 
 
 # ----------------------------------------------------------------------------- decode operators

@@ -10,6 +10,10 @@ Per step, for the B rows (decode rows first):
     positions 0 .. pos[r] of its sequence) -> O matmul -> add + RMSNorm -> fused gate/up matmul ->
     SwiGLU (rows) -> down matmul
     -> add + final RMSNorm -> classifier matmul on the decode rows only -> argmax per row.
+Where the matmul kernel for B rows fuses epilogues (the prefill GEMM, sq8_epilogue_fused), the
+residual adds run in the O and down matmuls' output stage (in place on the residual stream x,
+followed by a plain RMSNorm) and the SwiGLU in the gate/up matmul's, as
+sq8_matmul_epilogue does.
 
 All rows write their KV before any row attends, so prefill rows of one sequence in the same step
 see each other causally. The KV pool is [layers][num_blocks][block_size][kv_dim] fp32 for keys
@@ -21,8 +25,9 @@ from typing import List
 
 import numpy as np
 
-from . import (Workspace, add_rmsnorm, argmax_rows, embedding, matmul, paged_attention,
-               paged_rope_kv, rmsnorm, rope_tables, swiglu_rows)
+from . import (SQ8_EPI_RESIDUAL, SQ8_EPI_SWIGLU, Workspace, add_rmsnorm, argmax_rows, embedding,
+               epilogue_fused, matmul, matmul_epilogue, paged_attention, paged_rope_kv, rmsnorm,
+               rope_tables, swiglu_rows)
 
 EPS = 1e-6
 
@@ -59,6 +64,7 @@ class PagedBatchModel:
         self.next = torch.zeros(R, **i32)
         self.ws = Workspace(device)
         self.rows_run = 0
+        self._fuse = {}
 
     @classmethod
     def from_decoder(cls, dec, max_rows: int, max_seq_len: int, num_blocks: int,
@@ -73,6 +79,20 @@ class PagedBatchModel:
     def _mm(self, x, qs, y, stream):
         q, s = qs
         matmul(x, q, s, y, group_size=self.gs, workspace=self.ws, stream=stream)
+
+    def _mm_epi(self, x, qs, y, epilogue, stream, residual=None):
+        q, s = qs
+        matmul_epilogue(x, q, s, y, epilogue, residual=residual, group_size=self.gs,
+                        workspace=self.ws, stream=stream)
+
+    def fused(self, B: int):
+        """(O, gate/up, down) epilogues fused at B rows."""
+        if B not in self._fuse:
+            cfg, gs = self.cfg, self.gs
+            d, h = cfg.dim, cfg.hidden_dim
+            self._fuse[B] = (epilogue_fused(B, d, d, gs), epilogue_fused(B, 2 * h, d, gs),
+                             epilogue_fused(B, d, h, gs))
+        return self._fuse[B]
 
     def forward(self, rows, tables: List[List[int]]) -> List[int]:
         """Run the batch rows (scheduler.BatchRow, decode rows first) and return the greedy token
@@ -106,25 +126,42 @@ class PagedBatchModel:
         x, xn, qkv, att = self.x[:B], self.xn[:B], self.qkv[:B], self.att[:B]
         proj, gu, hid = self.proj[:B], self.gu[:B], self.hid[:B]
         pos, table = self.pos[:B], self.table[:B]
+        fuse_o, fuse_gu, fuse_down = self.fused(B)
         embedding(w["emb"], self.tok[:B], x, stream=stream)
+        pending = False  # proj holds the FFN output still to be added to x
         for l in range(L):
-            if l == 0:
-                rmsnorm(x, w["norm"][0], xn, EPS, stream=stream)
-            else:  # residual of the previous FFN, then this layer's attention norm
+            if pending:  # residual of the previous FFN, then this layer's attention norm
                 add_rmsnorm(x, proj, w["norm"][l], xn, EPS, stream=stream)
+            else:
+                rmsnorm(x, w["norm"][l], xn, EPS, stream=stream)
             self._mm(xn, w["qkv"][l], qkv, stream)
             paged_rope_kv(qkv, cfg.head_num, cfg.kv_head_num, self.hs, pos, table,
                           self.block_size, self.sin, self.cos, self.kcache[l], self.vcache[l],
                           stream=stream)
             paged_attention(qkv, d + 2 * kv, cfg.head_num, cfg.kv_head_num, self.hs, pos, table,
                             self.block_size, self.kcache[l], self.vcache[l], att, stream=stream)
-            self._mm(att, w["o"][l], proj, stream)
-            add_rmsnorm(x, proj, w["norm"][L + l], xn, EPS, stream=stream)
-            self._mm(xn, w["gu"][l], gu, stream)
-            swiglu_rows(gu, hid, stream=stream)
-            self._mm(hid, w["down"][l], proj, stream)
+            if fuse_o:
+                self._mm_epi(att, w["o"][l], x, SQ8_EPI_RESIDUAL, stream, residual=x)
+                rmsnorm(x, w["norm"][L + l], xn, EPS, stream=stream)
+            else:
+                self._mm(att, w["o"][l], proj, stream)
+                add_rmsnorm(x, proj, w["norm"][L + l], xn, EPS, stream=stream)
+            if fuse_gu:
+                self._mm_epi(xn, w["gu"][l], hid, SQ8_EPI_SWIGLU, stream)
+            else:
+                self._mm(xn, w["gu"][l], gu, stream)
+                swiglu_rows(gu, hid, stream=stream)
+            if fuse_down:
+                self._mm_epi(hid, w["down"][l], x, SQ8_EPI_RESIDUAL, stream, residual=x)
+                pending = False
+            else:
+                self._mm(hid, w["down"][l], proj, stream)
+                pending = True
         if nd > 0:
-            add_rmsnorm(self.x[:nd], self.proj[:nd], w["norm"][2 * L], self.xn[:nd], EPS,
-                        stream=stream)
+            if pending:
+                add_rmsnorm(self.x[:nd], self.proj[:nd], w["norm"][2 * L], self.xn[:nd], EPS,
+                            stream=stream)
+            else:
+                rmsnorm(self.x[:nd], w["norm"][2 * L], self.xn[:nd], EPS, stream=stream)
             self._mm(self.xn[:nd], w["cls"], self.logits[:nd], stream)
             argmax_rows(self.logits[:nd], self.next[:nd], stream=stream)

@@ -70,6 +70,55 @@ size_t sq8_workspace_bytes(int M, int N, int K, int group_size) {
   return sq8::mfma_workspace_bytes(M, N, K);
 }
 
+static size_t align_up(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+// Where an unfused epilogue keeps the product: after the path's own buffers and never in the
+// ticket area (a workspace may be shared with MFMA calls whose tickets must stay zero).
+static size_t product_offset(size_t base) {
+  return align_up(base > sq8::kWsTicketBytes ? base : sq8::kWsTicketBytes);
+}
+
+int sq8_epilogue_fused(int M, int N, int K, int group_size) {
+  if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0) return 0;
+  return choose(M, N, K, group_size, true) == Path::kMfma && sq8::mfma_fuses_epilogue(M, N, K);
+}
+
+size_t sq8_epilogue_workspace_bytes(int M, int N, int K, int group_size, int epilogue) {
+  const size_t base = sq8_workspace_bytes(M, N, K, group_size);
+  if (epilogue == SQ8_EPI_NONE || sq8_epilogue_fused(M, N, K, group_size)) return base;
+  return product_offset(base) + static_cast<size_t>(M) * N * sizeof(float);
+}
+
+int sq8_matmul_epilogue(const float* x, const int8_t* w, const float* scales, float* y, int M,
+                        int N, int K, int group_size, int epilogue, const float* residual,
+                        void* workspace, size_t workspace_bytes, void* hip_stream) {
+  if (epilogue == SQ8_EPI_NONE)
+    return sq8_matmul(x, w, scales, y, M, N, K, group_size, workspace, workspace_bytes,
+                      hip_stream);
+  if (epilogue != SQ8_EPI_RESIDUAL && epilogue != SQ8_EPI_SWIGLU) return SQ8_ERR_DIMS;
+  const int v = validate(x, w, scales, y, M, N, K, group_size);
+  if (v != SQ8_OK) return v;
+  if (epilogue == SQ8_EPI_RESIDUAL && !residual) return SQ8_ERR_NULL;
+  if (epilogue == SQ8_EPI_SWIGLU && N % 2 != 0) return SQ8_ERR_DIMS;
+  const size_t need = sq8_epilogue_workspace_bytes(M, N, K, group_size, epilogue);
+  if (workspace_bytes < need || (need > 0 && workspace == nullptr)) return SQ8_ERR_WORKSPACE;
+  hipStream_t st = static_cast<hipStream_t>(hip_stream);
+  const sq8::Epi epi{epilogue, residual};
+  const bool aligned = aligned16(x) && aligned16(w);
+  hipError_t e;
+  if (aligned && sq8_epilogue_fused(M, N, K, group_size)) {
+    e = sq8::launch_mfma(x, w, scales, y, M, N, K, group_size, workspace, st, epi);
+    return e == hipSuccess ? SQ8_OK : SQ8_ERR_LAUNCH;
+  }
+  // Unfused: the product goes to the workspace after the path's own buffers.
+  const size_t base = sq8_workspace_bytes(M, N, K, group_size);
+  float* t = reinterpret_cast<float*>(static_cast<char*>(workspace) + product_offset(base));
+  const int r = sq8_matmul(x, w, scales, t, M, N, K, group_size, workspace, base, hip_stream);
+  if (r != SQ8_OK) return r;
+  e = sq8::launch_epilogue(t, y, M, N, epi, st);
+  return e == hipSuccess ? SQ8_OK : SQ8_ERR_LAUNCH;
+}
+
 const char* sq8_status_string(int status) {
   switch (status) {
     case SQ8_OK: return "ok";

@@ -9,13 +9,36 @@ constexpr int kWave = 64;  // CDNA wavefront width
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));  // 16 int8 weights as one dwordx4
 
+// Output epilogue of a matmul (the values match enum sq8_epilogue in include/sq8.h).
+constexpr int kEpiNone = 0;
+constexpr int kEpiResidual = 1;  // y = res + x.W^T (res may alias y)
+constexpr int kEpiSwiglu = 2;    // W = [w1; w3] (N = 2F rows): y[M][F] = silu(x.w1^T) * (x.w3^T)
+struct Epi {
+  int mode;
+  const float* res;
+};
+
+// silu(g) * u, written as the SwiGLU operator computes it: (g * 1/(1 + e^-g)) * u.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float sig = 1.0f / (1.0f + expf(-g));
+  return (g * sig) * u;
+}
+
+// Bytes of split-K tickets at the start of every MFMA workspace. They must be zero before the
+// first call and every call leaves them zero, so no other use of a workspace may write there.
+constexpr int kWsTicketBytes = 64 * 1024;
+
 // Launchers (host side). Each returns hipSuccess or the launch error.
 hipError_t launch_gemv(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
                        int K, int gs, hipStream_t st);
 int cu_count();
 size_t mfma_workspace_bytes(int M, int N, int K);
+// y = epilogue(x.W^T) (y is [M][N/2] for SwiGLU). Only when mfma_fuses_epilogue(M, N, K); other
+// shapes take launch_mfma with epi.mode == kEpiNone and then launch_epilogue.
 hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
-                       int K, int gs, void* ws, hipStream_t st);
+                       int K, int gs, void* ws, hipStream_t st, Epi epi = Epi{kEpiNone, nullptr});
+bool mfma_fuses_epilogue(int M, int N, int K);
+hipError_t launch_epilogue(const float* t, float* y, int M, int N, Epi epi, hipStream_t st);
 bool gemv_stream_fits(int M, int K);
 hipError_t launch_gemv_norm(const float* x, const float* res, float* x_out, const float* nw,
                             float eps, const int8_t* w, const float* s, float* y, int N, int K,

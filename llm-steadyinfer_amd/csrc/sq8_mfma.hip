@@ -166,8 +166,9 @@ struct PTile {
 template <int WAVES_M, int WAVES_N, int TM, int TN, int STAGES>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
     const _Float16* xh, const _Float16* xl, const float* __restrict__ rscale, const int8_t* w,
-    const float* s, float* __restrict__ out, int M, int N, int K, int gs, int groups_per_split) {
+    const float* s, float* out, int M, int N, int K, int gs, int groups_per_split, Epi epi) {
   using T = PTile<WAVES_M, WAVES_N, TM, TN, STAGES>;
+  static_assert(TN == 2, "SwiGLU pairs tile 0 (gate) with tile 1 (up) of a wave");
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -177,6 +178,15 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
   const int st_begin = blockIdx.z * groups_per_split;
   const int st_end = min(nsteps, st_begin + groups_per_split);
   const int gpr = K / gs;
+  // Weight row behind tile column c (0 <= c < BN). SwiGLU: the workgroup owns features
+  // f0 .. f0 + BN/2 - 1 of F = N/2; the wave's first 32-column tile holds their gate rows and the
+  // second their up rows (F rows further on), so one lane holds both halves of each output.
+  const bool swiglu = epi.mode == kEpiSwiglu;
+  const int F = N / 2, f0 = blockIdx.x * (T::BN / 2);
+  auto wrow = [&](int c) __attribute__((always_inline)) {
+    if (!swiglu) return min(n0 + c, N - 1);
+    return min(f0 + (c >> 6) * 32 + (c & 31), F - 1) + ((c >> 5) & 1) * F;
+  };
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
 
   // Per-thread DMA sources (byte offsets; the K offset of a stage is added to the base pointer).
@@ -191,13 +201,13 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
   for (int i = 0; i < T::WL; ++i) {
     const int slot = (i * T::NW + wave) * kWave + lane;
     const int r = slot >> 2, q = (slot & 3) ^ swz_w(slot >> 2);
-    woff[i] = static_cast<uint32_t>(min(n0 + r, N - 1)) * K + q * 16u;
+    woff[i] = static_cast<uint32_t>(wrow(r)) * K + q * 16u;
   }
 #pragma unroll
   for (int i = 0; i < T::SL; ++i) {
     const int run = i * T::NW + wave;            // 32-column run of this instruction
     const int c = run * 32 + (lane & 31);
-    soff[i] = static_cast<uint32_t>(min(n0 + c, N - 1)) * gpr * 4u;
+    soff[i] = static_cast<uint32_t>(wrow(c)) * gpr * 4u;
   }
   auto issue = [&](int st, int buf) __attribute__((always_inline)) {
     const uint32_t sb = lds0 + buf * T::STAGE;
@@ -304,7 +314,25 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
   // Drain the clamped tail loads before the workgroup's LDS is released.
   wait_vmcnt<0>();
 
-  float* dst = out + static_cast<size_t>(blockIdx.z) * M * N;
+  if (gridDim.z > 1) {  // split-K partial tile: raw sums at the weight row's column
+    float* dst = out + static_cast<size_t>(blockIdx.z) * M * N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + (wm * TM + i) * 32 + 8 * (r >> 2) + half * 4 + (r & 3);
+        if (m >= M) continue;
+        const float rsc = rscale[m];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int c = (wn * TN + j) * 32 + lrow;
+          const bool in = swiglu ? f0 + (c >> 6) * 32 + (c & 31) < F : n0 + c < N;
+          if (in) dst[static_cast<size_t>(m) * N + wrow(c)] = acc[i][j][r] * rsc;
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -312,17 +340,26 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
       const int m = m0 + (wm * TM + i) * 32 + 8 * (r >> 2) + half * 4 + (r & 3);
       if (m >= M) continue;
       const float rsc = rscale[m];
+      if (swiglu) {
+        const int f = f0 + wn * 32 + lrow;
+        if (f < F)
+          out[static_cast<size_t>(m) * F + f] = silu_mul(acc[i][0][r] * rsc, acc[i][TN - 1][r] * rsc);
+        continue;
+      }
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int n = n0 + (wn * TN + j) * 32 + lrow;
-        if (n < N) dst[static_cast<size_t>(m) * N + n] = acc[i][j][r] * rsc;
+        if (n >= N) continue;
+        const size_t o = static_cast<size_t>(m) * N + n;
+        const float v = acc[i][j][r] * rsc;
+        out[o] = epi.mode == kEpiResidual ? epi.res[o] + v : v;
       }
     }
   }
 }
 
 // Split-K tickets live at the start of the workspace; each call leaves them zero.
-constexpr int kTicketBytes = 64 * 1024;  // ticket array at the start of the workspace
+constexpr int kTicketBytes = kWsTicketBytes;  // ticket array at the start of the workspace
 // K groups per split of the tile kernel: bounds its LDS scale stage (16*T rows x this many).
 constexpr int kTileScaleGroups = 128;
 
@@ -1077,15 +1114,48 @@ __global__ __launch_bounds__(W * kWave) void tile_kernel(
     __hip_atomic_store(&tickets[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Sum split-K partials in split order: y[i] = sum_z part[z][i].
+// Sum split-K partials in split order, y[i] = sum_z part[z][i], then apply the epilogue:
+// residual: y[i] = res[i] + sum; SwiGLU (part holds M rows of N = 2F): y[m][f] =
+// silu(gate sum) * (up sum).
 __global__ __launch_bounds__(kThreads) void splitk_reduce_kernel(const float* __restrict__ part,
-                                                                float* __restrict__ y,
-                                                                size_t count, int splits) {
+                                                                float* y, int M, int N,
+                                                                int splits, Epi epi) {
+  const size_t mn = static_cast<size_t>(M) * N;
+  const bool swiglu = epi.mode == kEpiSwiglu;
+  const int F = N / 2;
+  const size_t count = swiglu ? static_cast<size_t>(M) * F : mn;
   for (size_t i = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x; i < count;
        i += static_cast<size_t>(gridDim.x) * kThreads) {
+    if (swiglu) {
+      const size_t g = (i / F) * N + i % F;
+      float a = part[g], b = part[g + F];
+      for (int z = 1; z < splits; ++z) {
+        a += part[z * mn + g];
+        b += part[z * mn + g + F];
+      }
+      y[i] = silu_mul(a, b);
+      continue;
+    }
     float v = part[i];
-    for (int z = 1; z < splits; ++z) v += part[static_cast<size_t>(z) * count + i];
-    y[i] = v;
+    for (int z = 1; z < splits; ++z) v += part[static_cast<size_t>(z) * mn + i];
+    y[i] = epi.mode == kEpiResidual ? epi.res[i] + v : v;
+  }
+}
+
+// Epilogue of the paths without a fused one: y = epilogue(t) for the finished product t [M][N].
+__global__ __launch_bounds__(kThreads) void epilogue_kernel(const float* __restrict__ t, float* y,
+                                                           int M, int N, Epi epi) {
+  const bool swiglu = epi.mode == kEpiSwiglu;
+  const int F = N / 2;
+  const size_t count = swiglu ? static_cast<size_t>(M) * F : static_cast<size_t>(M) * N;
+  for (size_t i = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x; i < count;
+       i += static_cast<size_t>(gridDim.x) * kThreads) {
+    if (swiglu) {
+      const size_t g = (i / F) * N + i % F;
+      y[i] = silu_mul(t[g], t[g + F]);
+    } else {
+      y[i] = epi.res[i] + t[i];
+    }
   }
 }
 
@@ -1180,7 +1250,7 @@ Plan make_plan(int M, int N, int K) {
 template <int WM, int WN, int TM, int TN, int STAGES>
 hipError_t launch_gemm(const _Float16* xh, const _Float16* xl, const float* rsc,
                             const int8_t* w, const float* s, float* out, int M, int N, int K,
-                            int gs, const Plan& p, hipStream_t st) {
+                            int gs, const Plan& p, hipStream_t st, Epi epi) {
   using T = PTile<WM, WN, TM, TN, STAGES>;
   auto kern = gemm_kernel<WM, WN, TM, TN, STAGES>;
   static bool attr_set = false;  // LDS above 64 KiB needs the opt-in attribute
@@ -1191,9 +1261,12 @@ hipError_t launch_gemm(const _Float16* xh, const _Float16* xl, const float* rsc,
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  const dim3 grid((N + T::BN - 1) / T::BN, (M + T::BM - 1) / T::BM, p.splits);
+  // SwiGLU: a workgroup owns BN/2 features (their gate and up rows)
+  const int cols = epi.mode == kEpiSwiglu ? (N / 2 + T::BN / 2 - 1) / (T::BN / 2)
+                                          : (N + T::BN - 1) / T::BN;
+  const dim3 grid(cols, (M + T::BM - 1) / T::BM, p.splits);
   hipLaunchKernelGGL(kern, grid, dim3(T::NT), T::LDS_BYTES, st, xh, xl, rsc, w, s, out, M, N, K,
-                     gs, p.groups_per_split);
+                     gs, p.groups_per_split, epi);
   return hipGetLastError();
 }
 
@@ -1270,9 +1343,22 @@ size_t mfma_workspace_bytes(int M, int N, int K) {
 
 // Requires: K % 64 == 0, group_size % 64 == 0, K % group_size == 0, 16-byte aligned x and w,
 // workspace of mfma_workspace_bytes(M, N, K).
-hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
-                       int K, int gs, void* ws, hipStream_t st) {
+bool mfma_fuses_epilogue(int M, int N, int K) {
   const Plan p = make_plan(M, N, K);
+  return !p.tile && !p.skinny;
+}
+
+hipError_t launch_epilogue(const float* t, float* y, int M, int N, Epi epi, hipStream_t st) {
+  const size_t count = static_cast<size_t>(M) * (epi.mode == kEpiSwiglu ? N / 2 : N);
+  const int grid = static_cast<int>(std::min<size_t>((count + kThreads - 1) / kThreads, 4096));
+  hipLaunchKernelGGL(epilogue_kernel, dim3(grid), dim3(kThreads), 0, st, t, y, M, N, epi);
+  return hipGetLastError();
+}
+
+hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
+                       int K, int gs, void* ws, hipStream_t st, Epi epi) {
+  const Plan p = make_plan(M, N, K);
+  if (epi.mode != kEpiNone && (p.tile || p.skinny)) return hipErrorInvalidValue;
   unsigned* tickets = static_cast<unsigned*>(ws);
   char* base = static_cast<char*>(ws) + kTicketBytes;
   if (p.tile) {
@@ -1324,14 +1410,14 @@ hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (p.cfg == 1)
-    e = launch_gemm<1, 4, 2, 2, 3>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st);
+    e = launch_gemm<1, 4, 2, 2, 3>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st, epi);
   else
-    e = launch_gemm<2, 4, 2, 2, 3>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st);
+    e = launch_gemm<2, 4, 2, 2, 3>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st, epi);
   if (e != hipSuccess || p.splits == 1) return e;
-  const size_t count = static_cast<size_t>(M) * N;
+  const size_t count = static_cast<size_t>(M) * (epi.mode == kEpiSwiglu ? N / 2 : N);
   const int grid = static_cast<int>(std::min<size_t>((count + kThreads - 1) / kThreads, 4096));
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid), dim3(kThreads), 0, st, part, y, count,
-                     p.splits);
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid), dim3(kThreads), 0, st, part, y, M, N,
+                     p.splits, epi);
   return hipGetLastError();
 }
 

@@ -148,7 +148,7 @@ def test_swiglu_and_argmax_rows(sq8, dev):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("max_batch,block_size,num_blocks", [(4, 4, None), (4, 4, 20), (4, 4, 24),
-                                                           (8, 8, None)])
+                                                           (8, 8, None), (96, 8, None)])
 def test_continuous_batching_matches_oracle(dev, tmp_path, max_batch, block_size, num_blocks):
     """Six prompts (1..40 tokens) scheduled with chunked prefill mixed into decode steps (and,
     with a 20- or 24-block pool, preemption and recompute): every sequence's greedy tokens equal the
@@ -175,4 +175,6 @@ def test_continuous_batching_matches_oracle(dev, tmp_path, max_batch, block_size
     print("steps", s.steps, "rows", s.rows_run, "preemptions", s.preemptions)
     if num_blocks is not None:
         assert s.preemptions > 0
+    if max_batch > 64:  # the 88 prompt tokens start as one step: the fused-epilogue GEMM path
+        assert model.fused(88) == (True, True, True)
     assert got == ref

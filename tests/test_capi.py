@@ -83,3 +83,37 @@ def test_workspace_sizes(sq8):
         assert sq8.workspace_bytes(M, 4096, 4096, 64) > 0
     assert sq8.workspace_bytes(2048, 4096, 4096, 64) >= 4 * 2048 * 4096
     assert sq8.workspace_bytes(0, 4096, 4096, 64) == 0
+
+
+def epi_raw(sq8, x, w, s, y, M, N, K, gs, epi, res, ws=0, wsb=0):
+    return int(sq8.lib().sq8_matmul_epilogue(x or None, w or None, s or None, y or None, M, N, K,
+                                             gs, epi, res or None, ws or None, wsb, None))
+
+
+@pytest.mark.parametrize("M,N,K,epi,res,code", [
+    (128, 512, 1024, 1, 0, -1),        # residual epilogue without a residual
+    (128, 511, 1024, 2, 0, -2),        # SwiGLU needs the even N of a [w1; w3] weight
+    (128, 512, 1024, 7, 0, -2),        # unknown epilogue
+    (128, 512, 66, 2, 0, -2),          # the ordinary shape checks still apply
+    (128, 512, 1024, 2, 0, -4),        # no workspace
+    (4, 512, 1024, 1, FAKE, -4),       # unfused path: the product buffer is workspace too
+])
+def test_epilogue_argument_errors(sq8, M, N, K, epi, res, code):
+    assert epi_raw(sq8, FAKE, FAKE, FAKE, FAKE, M, N, K, 64, epi, res) == code
+
+
+def test_epilogue_fusion_and_workspace(sq8):
+    # the prefill GEMM fuses; decode paths run the product into the workspace first
+    assert sq8.epilogue_fused(2048, 28672, 4096)
+    assert sq8.epilogue_fused(64, 4096, 14336)
+    assert not sq8.epilogue_fused(1, 28672, 4096)
+    assert not sq8.epilogue_fused(16, 28672, 4096)
+    L = sq8.lib()
+    for M, N, K in ((1, 8192, 4096), (16, 8192, 4096), (2048, 8192, 4096)):
+        base = sq8.workspace_bytes(M, N, K, 64)
+        assert L.sq8_epilogue_workspace_bytes(M, N, K, 64, 0) == base
+        for e in (1, 2):
+            extra = L.sq8_epilogue_workspace_bytes(M, N, K, 64, e) - base
+            # the product never lands in the 64 KiB ticket area of MFMA workspaces
+            off = (max(base, 65536) + 255) // 256 * 256
+            assert extra == (0 if sq8.epilogue_fused(M, N, K) else off + M * N * 4 - base)
