@@ -168,7 +168,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
     const _Float16* xh, const _Float16* xl, const float* __restrict__ rscale, const int8_t* w,
     const float* s, float* out, int M, int N, int K, int gs, int groups_per_split, Epi epi) {
   using T = PTile<WAVES_M, WAVES_N, TM, TN, STAGES>;
-  static_assert(TN == 2, "SwiGLU pairs tile 0 (gate) with tile 1 (up) of a wave");
+  static_assert(TN % 2 == 0, "SwiGLU pairs tile j (gate) with tile j + TN/2 (up) of a wave");
+  constexpr int HT = TN / 2;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -179,13 +180,18 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
   const int st_end = min(nsteps, st_begin + groups_per_split);
   const int gpr = K / gs;
   // Weight row behind tile column c (0 <= c < BN). SwiGLU: the workgroup owns features
-  // f0 .. f0 + BN/2 - 1 of F = N/2; the wave's first 32-column tile holds their gate rows and the
-  // second their up rows (F rows further on), so one lane holds both halves of each output.
+  // f0 .. f0 + BN/2 - 1 of F = N/2; a wave's 32-column tiles j < TN/2 hold the gate rows of its
+  // features and tiles j + TN/2 their up rows (F rows further on), so one lane holds both halves
+  // of each output.
   const bool swiglu = epi.mode == kEpiSwiglu;
   const int F = N / 2, f0 = blockIdx.x * (T::BN / 2);
+  auto feat = [&](int c) __attribute__((always_inline)) {  // SwiGLU feature of tile column c
+    const int tl = c >> 5, jj = (tl % TN) % HT;
+    return f0 + ((tl / TN) * HT + jj) * 32 + (c & 31);
+  };
   auto wrow = [&](int c) __attribute__((always_inline)) {
     if (!swiglu) return min(n0 + c, N - 1);
-    return min(f0 + (c >> 6) * 32 + (c & 31), F - 1) + ((c >> 5) & 1) * F;
+    return min(feat(c), F - 1) + (((c >> 5) % TN) >= HT ? F : 0);
   };
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
 
@@ -214,7 +220,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
     const char* xhb = reinterpret_cast<const char*>(xh) + static_cast<size_t>(st) * BK * 2;
     const char* xlb = reinterpret_cast<const char*>(xl) + static_cast<size_t>(st) * BK * 2;
     const char* wb = reinterpret_cast<const char*>(w) + static_cast<size_t>(st) * BK;
-    const char* sbp = reinterpret_cast<const char*>(s) + static_cast<size_t>(st * BK / gs) * 4;
+    const int sg = gs == BK ? st : st * BK / gs;  // scale column of this group
+    const char* sbp = reinterpret_cast<const char*>(s) + static_cast<size_t>(sg) * 4;
 #pragma unroll
     for (int i = 0; i < T::XL; ++i) {
       const uint32_t d = ((i * T::NW + wave) * kWave) * 16;
@@ -256,12 +263,20 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
 #pragma unroll
     for (int p = 0; p < STAGES - 1; ++p) issue(min(st_begin + p, st_end - 1), p);
   }
-  for (int st = st_begin; st < st_end; ++st) {
-    const int rel = st - st_begin;
+  // One 64-wide group: wait for its stage, refill the stage read last time, multiply into pn, and
+  // meanwhile fold the previous group's product po (scale so) into the accumulators, so that
+  // those FMAs overlap this group's MFMAs instead of waiting for them.
+  int cur = 0, nxt = STAGES - 1;
+  // Two product buffers fit the register file only for up to 4 tiles per wave.
+  constexpr bool kOverlap = TM * TN <= 4;
+  auto group = [&](int st, f16v (&pn)[TM][TN], float (&sn)[TN], const f16v (&po)[TM][TN],
+                   const float (&so)[TN]) __attribute__((always_inline)) {
     wait_vmcnt<(STAGES - 2) * T::LOADS>();
     __syncthreads();
-    issue(min(st + STAGES - 1, st_end - 1), (rel + STAGES - 1) % STAGES);
-    const char* sp = smem + (rel % STAGES) * T::STAGE;
+    issue(min(st + STAGES - 1, st_end - 1), nxt);
+    const char* sp = smem + cur * T::STAGE;
+    cur = cur == STAGES - 1 ? 0 : cur + 1;
+    nxt = nxt == STAGES - 1 ? 0 : nxt + 1;
     h8 bw[TN][4];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
@@ -279,10 +294,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
         bw[j][2 * u + 1] = __builtin_bit_cast(h8, b);
       }
     }
-    float sc[TN];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) sc[j] = *reinterpret_cast<const float*>(sp + scoff[j]);
-    f16v p[TM][TN];
+    for (int j = 0; j < TN; ++j) sn[j] = *reinterpret_cast<const float*>(sp + scoff[j]);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       h8 ah[TM], al[TM];
@@ -297,19 +310,59 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
         for (int j = 0; j < TN; ++j) {
           if (t == 0) {
             const f16v zero = {};
-            p[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j][t], zero, 0, 0, 0);
+            pn[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j][t], zero, 0, 0, 0);
           } else {
-            p[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j][t], p[i][j], 0, 0, 0);
+            pn[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], bw[j][t], pn[i][j], 0, 0, 0);
           }
-          p[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bw[j][t], p[i][j], 0, 0, 0);
+          pn[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], bw[j][t], pn[i][j], 0, 0, 0);
         }
+      // a quarter of the previous group's FMAs per K step
+      if constexpr (kOverlap) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 4 * t; r < 4 * t + 4; ++r)
+              acc[i][j][r] = fmaf(so[j], po[i][j][r], acc[i][j][r]);
+      }
     }
+  };
+  auto fold = [&](const f16v (&po)[TM][TN], const float (&so)[TN]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(sc[j], p[i][j][r], acc[i][j][r]);
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = fmaf(so[j], po[i][j][r], acc[i][j][r]);
+  };
+  f16v p0[TM][TN], p1[TM][TN];
+  float s0[TN], s1[TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      s0[j] = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) p0[i][j][r] = 0.f;
+    }
+  if constexpr (!kOverlap) {  // one product buffer: fold each group right after its MFMAs
+    for (int st = st_begin; st < st_end; ++st) {
+      group(st, p1, s1, p0, s0);
+      fold(p1, s1);
+    }
+  } else {  // p0 and p1 alternate (p0 starts as a zero product)
+    int st = st_begin;
+    for (; st + 1 < st_end; st += 2) {
+      group(st, p1, s1, p0, s0);
+      group(st + 1, p0, s0, p1, s1);
+    }
+    if (st < st_end) {
+      group(st, p1, s1, p0, s0);
+      fold(p1, s1);
+    } else {
+      fold(p0, s0);
+    }
   }
   // Drain the clamped tail loads before the workgroup's LDS is released.
   wait_vmcnt<0>();
@@ -326,7 +379,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
           const int c = (wn * TN + j) * 32 + lrow;
-          const bool in = swiglu ? f0 + (c >> 6) * 32 + (c & 31) < F : n0 + c < N;
+          const bool in = swiglu ? feat(c) < F : n0 + c < N;
           if (in) dst[static_cast<size_t>(m) * N + wrow(c)] = acc[i][j][r] * rsc;
         }
       }
@@ -341,9 +394,13 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
       if (m >= M) continue;
       const float rsc = rscale[m];
       if (swiglu) {
-        const int f = f0 + wn * 32 + lrow;
-        if (f < F)
-          out[static_cast<size_t>(m) * F + f] = silu_mul(acc[i][0][r] * rsc, acc[i][TN - 1][r] * rsc);
+#pragma unroll
+        for (int jj = 0; jj < HT; ++jj) {
+          const int f = f0 + (wn * HT + jj) * 32 + lrow;
+          if (f < F)
+            out[static_cast<size_t>(m) * F + f] =
+                silu_mul(acc[i][jj][r] * rsc, acc[i][jj + HT][r] * rsc);
+        }
         continue;
       }
 #pragma unroll
