@@ -244,6 +244,9 @@ def main():
     ap.add_argument("--graph", action="store_true", help="replay the step as one HIP graph")
     ap.add_argument("--profile", action="store_true",
                     help="short run for counter collection: a 256 MiB copy, then 5 decode steps")
+    ap.add_argument("--profile-prefill", action="store_true",
+                    help="short run for counter collection: the four config-3 prefill GEMMs "
+                         "(M = 2048), 3 launches each")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path. The matmul "
@@ -289,6 +292,18 @@ def main():
     def step():
         for c in calls:
             c()
+
+    if args.profile_prefill:
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        for p, (N, K) in PROJ.items():
+            x, y = xbuf(2048, K), torch.empty((2048, N), device=dev)
+            for l in range(3):
+                Call(sq8, x, *weights[p][l], y, stream, ws)()
+            torch.cuda.synchronize()
+        print(json.dumps({"profile_run": "prefill", "M": 2048, "launches_per_shape": 3}))
+        return
 
     if args.profile:
         # Calibration copy of known size for FETCH_SIZE / WRITE_SIZE, then a few decode steps.
@@ -372,6 +387,22 @@ def main():
                 del x, y, cs
             print(f"# sweep M={M} done", file=sys.stderr, flush=True)
 
+    # Config 3 (prefill, M = 2048): the GEMM is MFMA-bound. Issued f16 MFMA work is twice the
+    # useful multiply-adds (hi and lo activation halves); peak = dense f16 MFMA.
+    prefill = None
+    pre = [r for r in sweep if r["M"] == 2048]
+    if pre:
+        us = sum(r["us"] for r in pre)
+        flops = sum(2 * r["M"] * r["N"] * r["K"] for r in pre)
+        useful = flops / us / 1e6
+        prefill = {"bound": "mfma", "achieved": round(2 * useful, 1),
+                   "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                   "frac": round(2 * useful / MFMA_F16_PEAK_TFLOPS, 4),
+                   "useful_TFLOP/s": round(useful, 1),
+                   "kernel": "sq8 gemm_kernel<2,4,2,2,3> (128x256 tiles, LDS-DMA ring), "
+                             "M=2048 over the four Llama-3-8B projections",
+                   "us_per_layer": round(us, 1)}
+
     decode = None
     if not args.no_decode:
         decode = decode_run(torch)
@@ -405,6 +436,7 @@ def main():
         "batch": batch,
         "step_algo_bytes": step_bytes,
         "roofline": roofline,
+        "prefill_roofline": prefill,
         "cpu_baseline": cpu,
         "sweep": sweep,
     }
