@@ -106,8 +106,15 @@ __device__ __forceinline__ void i8x4_to_h4(uint32_t d, uint32_t& lo, uint32_t& h
 //    most (STAGES - 2) stages of its own loads are outstanding, then a barrier publishes all
 //    threads' loads. The same barrier tells every wave that the stage being refilled next has
 //    been read by all waves. One barrier per 64-wide group.
-__device__ __forceinline__ int swz_x(int r) { return (r ^ (r >> 3)) & 7; }
-__device__ __forceinline__ int swz_w(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+// GPS groups per stage: x rows of 8*GPS chunks, w rows of 4*GPS chunks.
+template <int GPS>
+__device__ __forceinline__ int swz_x(int r) {
+  return GPS == 1 ? (r ^ (r >> 3)) & 7 : r & 15;
+}
+template <int GPS>
+__device__ __forceinline__ int swz_w(int r) {
+  return GPS == 1 ? ((r >> 1) ^ (r >> 2)) & 3 : (r ^ (r >> 3)) & 7;
+}
 
 // One 16-byte global -> LDS copy per lane: lane i writes LDS [lds_base + 16 i]. m0 (the LDS
 // base register of the DMA) is saved and restored around the copy.
@@ -141,33 +148,36 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-template <int WAVES_M, int WAVES_N, int TM, int TN, int STAGES>
+template <int WAVES_M, int WAVES_N, int TM, int TN, int STAGES, int GPS>
 struct PTile {
   static constexpr int NW = WAVES_M * WAVES_N;
   static constexpr int NT = NW * kWave;
   static constexpr int BM = WAVES_M * TM * 32;
   static constexpr int BN = WAVES_N * TN * 32;
-  static constexpr int XB = BM * 128;            // bytes of x hi (or lo) per stage
-  static constexpr int WB = BN * 64;             // bytes of int8 weights per stage
-  static constexpr int SB = BN * 8;              // scale bytes per stage (each 32-column run twice)
+  static constexpr int KB = BK * GPS;            // K per stage
+  static constexpr int CX = 8 * GPS;             // 16-byte chunks per staged x row (hi or lo)
+  static constexpr int CW = 4 * GPS;             // 16-byte chunks per staged weight row
+  static constexpr int XB = BM * CX * 16;        // bytes of x hi (or lo) per stage
+  static constexpr int WB = BN * CW * 16;        // bytes of int8 weights per stage
+  static constexpr int SB = GPS * BN * 8;        // scale bytes per stage (each 32-column run twice)
   static constexpr int STAGE = 2 * XB + WB + SB;
   static constexpr size_t LDS_BYTES = static_cast<size_t>(STAGES) * STAGE;
-  static constexpr int XL = BM * 8 / NT;         // x DMA instructions per thread per stage (hi or lo)
-  static constexpr int WL = BN * 4 / NT;         // weight DMA instructions per thread per stage
-  static constexpr int SL = BN / 32 / NW;        // scale DMA instructions per thread per stage
+  static constexpr int XL = BM * CX / NT;        // x DMA instructions per thread per stage (hi or lo)
+  static constexpr int WL = BN * CW / NT;        // weight DMA instructions per thread per stage
+  static constexpr int SL = GPS * BN / 32 / NW;  // scale DMA instructions per thread per stage
   static constexpr int LOADS = 2 * XL + WL + SL;
-  static_assert(XL >= 1 && WL >= 1 && SL >= 1 && BM * 8 % NT == 0 && BN * 4 % NT == 0 &&
-                    (BN / 32) % NW == 0,
+  static_assert(XL >= 1 && WL >= 1 && SL >= 1 && BM * CX % NT == 0 && BN * CW % NT == 0 &&
+                    (GPS * BN / 32) % NW == 0,
                 "tile does not match the DMA pattern");
   static_assert((STAGES - 2) * LOADS < 64, "vmcnt range");
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 };
 
-template <int WAVES_M, int WAVES_N, int TM, int TN, int STAGES>
+template <int WAVES_M, int WAVES_N, int TM, int TN, int STAGES, int GPS>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
     const _Float16* xh, const _Float16* xl, const float* __restrict__ rscale, const int8_t* w,
     const float* s, float* out, int M, int N, int K, int gs, int groups_per_split, Epi epi) {
-  using T = PTile<WAVES_M, WAVES_N, TM, TN, STAGES>;
+  using T = PTile<WAVES_M, WAVES_N, TM, TN, STAGES, GPS>;
   static_assert(TN % 2 == 0, "SwiGLU pairs tile j (gate) with tile j + TN/2 (up) of a wave");
   constexpr int HT = TN / 2;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -175,7 +185,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int n0 = blockIdx.x * T::BN, m0 = blockIdx.y * T::BM;
-  const int nsteps = K / BK;
+  const int nsteps = K / T::KB;  // stages of GPS groups; the split is in stages
   const int st_begin = blockIdx.z * groups_per_split;
   const int st_end = min(nsteps, st_begin + groups_per_split);
   const int gpr = K / gs;
@@ -200,28 +210,26 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
 #pragma unroll
   for (int i = 0; i < T::XL; ++i) {
     const int slot = (i * T::NW + wave) * kWave + lane;
-    const int r = slot >> 3, c = (slot & 7) ^ swz_x(slot >> 3);
+    const int r = slot / T::CX, c = (slot % T::CX) ^ swz_x<GPS>(slot / T::CX);
     xoff[i] = static_cast<uint32_t>(min(m0 + r, M - 1)) * K * 2u + c * 16u;
   }
 #pragma unroll
   for (int i = 0; i < T::WL; ++i) {
     const int slot = (i * T::NW + wave) * kWave + lane;
-    const int r = slot >> 2, q = (slot & 3) ^ swz_w(slot >> 2);
+    const int r = slot / T::CW, q = (slot % T::CW) ^ swz_w<GPS>(slot / T::CW);
     woff[i] = static_cast<uint32_t>(wrow(r)) * K + q * 16u;
   }
 #pragma unroll
   for (int i = 0; i < T::SL; ++i) {
-    const int run = i * T::NW + wave;            // 32-column run of this instruction
+    const int run = (i * T::NW + wave) % (T::BN / 32);  // 32-column run of this instruction
     const int c = run * 32 + (lane & 31);
     soff[i] = static_cast<uint32_t>(wrow(c)) * gpr * 4u;
   }
   auto issue = [&](int st, int buf) __attribute__((always_inline)) {
     const uint32_t sb = lds0 + buf * T::STAGE;
-    const char* xhb = reinterpret_cast<const char*>(xh) + static_cast<size_t>(st) * BK * 2;
-    const char* xlb = reinterpret_cast<const char*>(xl) + static_cast<size_t>(st) * BK * 2;
-    const char* wb = reinterpret_cast<const char*>(w) + static_cast<size_t>(st) * BK;
-    const int sg = gs == BK ? st : st * BK / gs;  // scale column of this group
-    const char* sbp = reinterpret_cast<const char*>(s) + static_cast<size_t>(sg) * 4;
+    const char* xhb = reinterpret_cast<const char*>(xh) + static_cast<size_t>(st) * T::KB * 2;
+    const char* xlb = reinterpret_cast<const char*>(xl) + static_cast<size_t>(st) * T::KB * 2;
+    const char* wb = reinterpret_cast<const char*>(w) + static_cast<size_t>(st) * T::KB;
 #pragma unroll
     for (int i = 0; i < T::XL; ++i) {
       const uint32_t d = ((i * T::NW + wave) * kWave) * 16;
@@ -232,8 +240,12 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
     for (int i = 0; i < T::WL; ++i)
       dma16(wb, woff[i], sb + 2 * T::XB + ((i * T::NW + wave) * kWave) * 16);
 #pragma unroll
-    for (int i = 0; i < T::SL; ++i)
-      dma4(sbp, soff[i], sb + 2 * T::XB + T::WB + (i * T::NW + wave) * 256);
+    for (int i = 0; i < T::SL; ++i) {
+      const int g = st * GPS + (i * T::NW + wave) / (T::BN / 32);  // group of this instruction
+      const int sg = gs == BK ? g : g * BK / gs;                    // its scale column
+      dma4(reinterpret_cast<const char*>(s) + static_cast<size_t>(sg) * 4, soff[i],
+           sb + 2 * T::XB + T::WB + (i * T::NW + wave) * 256);
+    }
   };
 
   f16v acc[TM][TN];
@@ -250,12 +262,14 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int r = (wm * TM + i) * 32 + lrow;
-    aoff[i] = r * 128 + ((half * 4) ^ swz_x(r)) * 16;   // chunk t of the lane: aoff ^ (16 t)
+    // chunk (group gi, step t) of the lane: aoff ^ (16 (8 gi + t))
+    aoff[i] = r * (T::CX * 16) + ((half * 4) ^ swz_x<GPS>(r)) * 16;
   }
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int r = (wn * TN + j) * 32 + lrow;
-    boff[j] = 2 * T::XB + r * 64 + ((half * 2) ^ swz_w(r)) * 16;  // chunk 2h+u: boff ^ (16 u)
+    // chunk (group gi, half u): boff ^ (16 (4 gi + u))
+    boff[j] = 2 * T::XB + r * (T::CW * 16) + ((half * 2) ^ swz_w<GPS>(r)) * 16;
     scoff[j] = 2 * T::XB + T::WB + (r >> 5) * 256 + (r & 31) * 4;
   }
 
@@ -263,26 +277,30 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
 #pragma unroll
     for (int p = 0; p < STAGES - 1; ++p) issue(min(st_begin + p, st_end - 1), p);
   }
-  // One 64-wide group: wait for its stage, refill the stage read last time, multiply into pn, and
-  // meanwhile fold the previous group's product po (scale so) into the accumulators, so that
-  // those FMAs overlap this group's MFMAs instead of waiting for them.
+  // Wait for stage st, refill the stage read last time and return st's LDS address.
   int cur = 0, nxt = STAGES - 1;
-  // Two product buffers fit the register file only for up to 4 tiles per wave.
-  constexpr bool kOverlap = TM * TN <= 4;
-  auto group = [&](int st, f16v (&pn)[TM][TN], float (&sn)[TN], const f16v (&po)[TM][TN],
-                   const float (&so)[TN]) __attribute__((always_inline)) {
+  auto begin_stage = [&](int st) __attribute__((always_inline)) {
     wait_vmcnt<(STAGES - 2) * T::LOADS>();
     __syncthreads();
     issue(min(st + STAGES - 1, st_end - 1), nxt);
     const char* sp = smem + cur * T::STAGE;
     cur = cur == STAGES - 1 ? 0 : cur + 1;
     nxt = nxt == STAGES - 1 ? 0 : nxt + 1;
+    return sp;
+  };
+  // Two product buffers fit the register file only for up to 4 tiles per wave.
+  constexpr bool kOverlap = TM * TN <= 4;
+  // One 64-wide group gi of a stage: multiply into pn (scale sn) and meanwhile fold the previous
+  // group's product po (scale so) into the accumulators, so that those FMAs overlap this group's
+  // MFMAs instead of waiting for them.
+  auto group = [&](const char* sp, int gi, f16v (&pn)[TM][TN], float (&sn)[TN],
+                   const f16v (&po)[TM][TN], const float (&so)[TN]) __attribute__((always_inline)) {
     h8 bw[TN][4];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const u32x4 raw = *reinterpret_cast<const u32x4*>(sp + (boff[j] ^ (16 * u)));
+        const u32x4 raw = *reinterpret_cast<const u32x4*>(sp + (boff[j] ^ (16 * (4 * gi + u))));
         uint32_t h[8];
         i8x4_to_h4(raw.x, h[0], h[1]);
         i8x4_to_h4(raw.y, h[2], h[3]);
@@ -295,14 +313,15 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
       }
     }
 #pragma unroll
-    for (int j = 0; j < TN; ++j) sn[j] = *reinterpret_cast<const float*>(sp + scoff[j]);
+    for (int j = 0; j < TN; ++j)
+      sn[j] = *reinterpret_cast<const float*>(sp + scoff[j] + gi * T::BN * 8);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       h8 ah[TM], al[TM];
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
-        ah[i] = *reinterpret_cast<const h8*>(sp + (aoff[i] ^ (16 * t)));
-        al[i] = *reinterpret_cast<const h8*>(sp + T::XB + (aoff[i] ^ (16 * t)));
+        ah[i] = *reinterpret_cast<const h8*>(sp + (aoff[i] ^ (16 * (8 * gi + t))));
+        al[i] = *reinterpret_cast<const h8*>(sp + T::XB + (aoff[i] ^ (16 * (8 * gi + t))));
       }
 #pragma unroll
       for (int i = 0; i < TM; ++i)
@@ -348,17 +367,28 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
     }
   if constexpr (!kOverlap) {  // one product buffer: fold each group right after its MFMAs
     for (int st = st_begin; st < st_end; ++st) {
-      group(st, p1, s1, p0, s0);
-      fold(p1, s1);
+      const char* sp = begin_stage(st);
+#pragma unroll
+      for (int gi = 0; gi < GPS; ++gi) {
+        group(sp, gi, p1, s1, p0, s0);
+        fold(p1, s1);
+      }
     }
-  } else {  // p0 and p1 alternate (p0 starts as a zero product)
+  } else if constexpr (GPS == 2) {  // p1 and p0 alternate within each stage
+    for (int st = st_begin; st < st_end; ++st) {
+      const char* sp = begin_stage(st);
+      group(sp, 0, p1, s1, p0, s0);
+      group(sp, 1, p0, s0, p1, s1);
+    }
+    fold(p0, s0);
+  } else {  // p0 and p1 alternate over stage pairs (p0 starts as a zero product)
     int st = st_begin;
     for (; st + 1 < st_end; st += 2) {
-      group(st, p1, s1, p0, s0);
-      group(st + 1, p0, s0, p1, s1);
+      group(begin_stage(st), 0, p1, s1, p0, s0);
+      group(begin_stage(st + 1), 0, p0, s0, p1, s1);
     }
     if (st < st_end) {
-      group(st, p1, s1, p0, s0);
+      group(begin_stage(st), 0, p1, s1, p0, s0);
       fold(p1, s1);
     } else {
       fold(p0, s0);
@@ -1227,6 +1257,7 @@ struct Plan {
   bool skinny;
   int kw;         // skinny: K groups per chunk (divides groups_per_split)
   int cfg;        // GEMM: 1: 64x256 tile, 2: 128x256.  Skinny: 0: MT=1, 1: MT=2
+  int gps;        // GEMM: 64-wide groups per K stage (the split is counted in stages)
   int bm, bn;
   int splits;
   int groups_per_split;
@@ -1280,11 +1311,16 @@ Plan make_plan(int M, int N, int K) {
     p.splits = (chunks + cps - 1) / cps;
     return p;
   }
-  // Pipelined GEMM: one 64 x 256 (M <= 64) or 128 x 256 tile per workgroup, one workgroup per CU
-  // (its LDS ring takes ~100 or ~150 KiB). K is split when that evens out the rounds of
+  // Pipelined GEMM: one 64 x 256 (M <= 64; 2 stages of 2 groups, 136 KiB of LDS, or 3 stages
+  // of one group when K is an odd number of groups) or 128 x 256 tile (3 stages of one group,
+  // 150 KiB) per workgroup, one workgroup per CU. K is split when that evens out the rounds of
   // workgroups over the CUs: cost = rounds / splits plus a small charge per split for the
   // partial tiles and the reduction.
   p.cfg = M <= 64 ? 1 : 2;
+  // 64-row tiles stream weights: two groups per stage read each weight row 128 bytes (one L2
+  // line) at a time (Llama down projection at 64 rows: 46 against 51 us with one group).
+  p.gps = p.cfg == 1 && K % (2 * BK) == 0 ? 2 : 1;
+  const int nst = nsteps / p.gps;
   p.bm = M <= 64 ? 64 : 128;
   p.bn = 256;
   const int cus = cu_count();
@@ -1299,17 +1335,17 @@ Plan make_plan(int M, int N, int K) {
     const double cost = rounds / sp + charge * (sp - 1);
     if (cost < best - 1e-9) { best = cost; splits = sp; }
   }
-  p.groups_per_split = (nsteps + splits - 1) / splits;
-  p.splits = (nsteps + p.groups_per_split - 1) / p.groups_per_split;
+  p.groups_per_split = (nst + splits - 1) / splits;
+  p.splits = (nst + p.groups_per_split - 1) / p.groups_per_split;
   return p;
 }
 
-template <int WM, int WN, int TM, int TN, int STAGES>
+template <int WM, int WN, int TM, int TN, int STAGES, int GPS = 1>
 hipError_t launch_gemm(const _Float16* xh, const _Float16* xl, const float* rsc,
                             const int8_t* w, const float* s, float* out, int M, int N, int K,
                             int gs, const Plan& p, hipStream_t st, Epi epi) {
-  using T = PTile<WM, WN, TM, TN, STAGES>;
-  auto kern = gemm_kernel<WM, WN, TM, TN, STAGES>;
+  using T = PTile<WM, WN, TM, TN, STAGES, GPS>;
+  auto kern = gemm_kernel<WM, WN, TM, TN, STAGES, GPS>;
   static bool attr_set = false;  // LDS above 64 KiB needs the opt-in attribute
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -1467,7 +1503,9 @@ hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (p.cfg == 1)
-    e = launch_gemm<1, 4, 2, 2, 3>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st, epi);
+    e = p.gps == 1
+            ? launch_gemm<1, 4, 2, 2, 3>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st, epi)
+            : launch_gemm<2, 4, 1, 2, 2, 2>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st, epi);
   else
     e = launch_gemm<2, 4, 2, 2, 3>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st, epi);
   if (e != hipSuccess || p.splits == 1) return e;

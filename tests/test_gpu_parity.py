@@ -195,3 +195,15 @@ def test_split_k_tickets_return_to_zero(sq8, dev):
     ref = o.matmul_f64(x, np.ascontiguousarray(q[rows]),
                        np.ascontiguousarray(s.reshape(N, -1)[rows].reshape(-1)), 64)
     check(ys[0][:, rows], ref, "split-k M=16")
+
+
+@pytest.mark.parametrize("M", [33, 48, 64])
+@pytest.mark.parametrize("N,K,gs", [(300, 8192, 64), (256, 8256, 64), (200, 16384, 64),
+                                    (96, 8192, 128), (130, 14336, 64)])
+def test_gemm_64_row_tiles(sq8, dev, M, N, K, gs):
+    """33-64 token rows with long rows go to the 64 x 256 GEMM tile: two groups per LDS stage
+    when K is an even number of groups (8192, 16384, 14336), one group per stage otherwise (8256),
+    group size 128 across the two groups of a stage, and split-K over few column tiles."""
+    x, q, s = o.make_case(M, N, K, gs, seed=M * 11 + N + K)
+    print(f"case M={M} N={N} K={K} gs={gs} fused={sq8.epilogue_fused(M, N, K, gs)}", flush=True)
+    check(run(sq8, dev, x, q, s, gs), o.matmul_f64(x, q, s, gs), f"M={M} N={N} K={K} gs={gs}")
