@@ -38,45 +38,104 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------- activation split
-// One workgroup per token row: absmax, exponent, then hi/lo halves.
-__global__ __launch_bounds__(kThreads) void split_x_kernel(const float* __restrict__ x,
-                                                          _Float16* __restrict__ xh,
-                                                          _Float16* __restrict__ xl,
-                                                          float* __restrict__ rscale, int K) {
-  __shared__ float red[kThreads / kWave];
-  const int m = blockIdx.x, tid = threadIdx.x;
-  const float* xr = x + static_cast<size_t>(m) * K;
+// Threads and register-held float4 per thread of the row-split kernels: a row of up to
+// kSplitThreads * 4 * kSplitV values is read once, kept in registers while the workgroup finds
+// its absmax, and converted from there (one memory round trip); longer rows are read twice.
+constexpr int kSplitThreads = 512;
+constexpr int kSplitV = 8;
+
+// Power of two for a row of absmax `amax`: x * 2^e has its absmax in [2^13, 2^14).
+__device__ __forceinline__ int row_exponent(float amax) {
+  int e = 0;
+  if (amax > 0.f && amax <= 3.402823466e38f) {
+    int ex;
+    frexpf(amax, &ex);  // amax = f * 2^ex, f in [0.5, 1)
+    e = min(max(14 - ex, -126), 126);
+  }
+  return e;
+}
+
+__device__ __forceinline__ float absmax4(float4 v) {
+  return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+
+// Load a row (zeros when !live) and return its exponent; v holds the first kSplitV float4 of
+// the thread (k = (tid + i * kSplitThreads) * 4) when the row fits, else it is re-read later.
+__device__ __forceinline__ int load_row_exponent(const float* __restrict__ xr, int K, bool live,
+                                                 float4 (&v)[kSplitV], float* red) {
+  const int tid = threadIdx.x;
+  const bool regs = K <= kSplitThreads * 4 * kSplitV;
   float amax = 0.f;
-  for (int k = tid * 4; k < K; k += kThreads * 4) {
-    const float4 v = *reinterpret_cast<const float4*>(xr + k);
-    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+  if (regs) {
+#pragma unroll
+    for (int i = 0; i < kSplitV; ++i) {
+      const int k = (tid + i * kSplitThreads) * 4;
+      v[i] = live && k < K ? *reinterpret_cast<const float4*>(xr + k)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < kSplitV; ++i) amax = fmaxf(amax, absmax4(v[i]));
+  } else if (live) {
+    for (int k = tid * 4; k < K; k += kSplitThreads * 4)
+      amax = fmaxf(amax, absmax4(*reinterpret_cast<const float4*>(xr + k)));
   }
 #pragma unroll
   for (int off = 32; off >= 1; off /= 2) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
   if ((tid & (kWave - 1)) == 0) red[tid >> 6] = amax;
   __syncthreads();
-  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  int e = 0;
-  if (amax > 0.f && amax <= 3.402823466e38f) {
-    int ex;
-    frexpf(amax, &ex);           // amax = f * 2^ex, f in [0.5, 1)
-    e = min(max(14 - ex, -126), 126);
+  amax = red[0];
+#pragma unroll
+  for (int w = 1; w < kSplitThreads / kWave; ++w) amax = fmaxf(amax, red[w]);
+  return row_exponent(amax);
+}
+
+// Visit the row's float4 chunks with their start k: from registers when the row fits, else
+// re-read (zeros when !live).
+template <typename F>
+__device__ __forceinline__ void for_row_chunks(const float* __restrict__ xr, int K, bool live,
+                                               const float4 (&v)[kSplitV], F&& f) {
+  const int tid = threadIdx.x;
+  if (K <= kSplitThreads * 4 * kSplitV) {
+#pragma unroll
+    for (int i = 0; i < kSplitV; ++i) {
+      const int k = (tid + i * kSplitThreads) * 4;
+      if (k < K) f(k, v[i]);
+    }
+  } else {
+    for (int k = tid * 4; k < K; k += kSplitThreads * 4)
+      f(k, live ? *reinterpret_cast<const float4*>(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f));
   }
-  if (tid == 0) rscale[m] = ldexpf(1.f, -e);
+}
+
+// x * 2^e = hi + lo for four values.
+__device__ __forceinline__ void split4(float4 v, int e, _Float16 (&h)[4], _Float16 (&l)[4]) {
+  const float a[4] = {ldexpf(v.x, e), ldexpf(v.y, e), ldexpf(v.z, e), ldexpf(v.w, e)};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h[i] = static_cast<_Float16>(a[i]);
+    l[i] = static_cast<_Float16>(a[i] - static_cast<float>(h[i]));
+  }
+}
+
+// One workgroup per token row: absmax, exponent, then hi/lo halves.
+__global__ __launch_bounds__(kSplitThreads) void split_x_kernel(const float* __restrict__ x,
+                                                              _Float16* __restrict__ xh,
+                                                              _Float16* __restrict__ xl,
+                                                              float* __restrict__ rscale, int K) {
+  __shared__ float red[kSplitThreads / kWave];
+  const int m = blockIdx.x;
+  const float* xr = x + static_cast<size_t>(m) * K;
+  float4 v[kSplitV];
+  const int e = load_row_exponent(xr, K, true, v, red);
+  if (threadIdx.x == 0) rscale[m] = ldexpf(1.f, -e);
   _Float16* hr = xh + static_cast<size_t>(m) * K;
   _Float16* lr = xl + static_cast<size_t>(m) * K;
-  for (int k = tid * 4; k < K; k += kThreads * 4) {
-    const float4 v = *reinterpret_cast<const float4*>(xr + k);
-    const float a[4] = {ldexpf(v.x, e), ldexpf(v.y, e), ldexpf(v.z, e), ldexpf(v.w, e)};
+  for_row_chunks(xr, K, true, v, [&](int k, float4 c) {
     _Float16 h[4], l[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      h[i] = static_cast<_Float16>(a[i]);
-      l[i] = static_cast<_Float16>(a[i] - static_cast<float>(h[i]));
-    }
+    split4(c, e, h, l);
     *reinterpret_cast<uint2*>(hr + k) = *reinterpret_cast<const uint2*>(h);
     *reinterpret_cast<uint2*>(lr + k) = *reinterpret_cast<const uint2*>(l);
-  }
+  });
 }
 
 // 4 int8 (one dword) -> 4 exact f16 (two dwords), see file comment.
@@ -956,50 +1015,28 @@ __global__ __launch_bounds__(kThreads) void skinny_i8_kernel(
 //    as in the skinny kernels).
 // Per group and column tile: P = sum of the hi and lo MFMAs over both half-steps (from zero),
 // acc += scale[n, g] * P. Result lane l: column l%16, rows 16*rt + 4*(l/16) .. +3.
-__global__ __launch_bounds__(kThreads) void pack_x_kernel(const float* __restrict__ x,
-                                                         uint2* __restrict__ xp,
-                                                         float* __restrict__ rscale, int M, int K,
-                                                         int RT) {
-  __shared__ float red[kThreads / kWave];
-  const int m = blockIdx.x, tid = threadIdx.x;
+__global__ __launch_bounds__(kSplitThreads) void pack_x_kernel(const float* __restrict__ x,
+                                                             uint2* __restrict__ xp,
+                                                             float* __restrict__ rscale, int M,
+                                                             int K, int RT) {
+  __shared__ float red[kSplitThreads / kWave];
+  const int m = blockIdx.x;
   const int rt = m >> 4;
   const bool live = m < M;
   const float* xr = x + static_cast<size_t>(min(m, M - 1)) * K;
-  float amax = 0.f;
-  if (live)
-    for (int k = tid * 4; k < K; k += kThreads * 4) {
-      const float4 v = *reinterpret_cast<const float4*>(xr + k);
-      amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
-#pragma unroll
-  for (int off = 32; off >= 1; off /= 2) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
-  if ((tid & (kWave - 1)) == 0) red[tid >> 6] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  int e = 0;
-  if (amax > 0.f && amax <= 3.402823466e38f) {
-    int ex;
-    frexpf(amax, &ex);  // amax = f * 2^ex, f in [0.5, 1)
-    e = min(max(14 - ex, -126), 126);
-  }
-  if (live && tid == 0) rscale[m] = ldexpf(1.f, -e);
-  for (int k = tid * 4; k < K; k += kThreads * 4) {
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (live) v = *reinterpret_cast<const float4*>(xr + k);
-    const float a[4] = {ldexpf(v.x, e), ldexpf(v.y, e), ldexpf(v.z, e), ldexpf(v.w, e)};
+  float4 v[kSplitV];
+  const int e = load_row_exponent(xr, K, live, v, red);
+  if (live && threadIdx.x == 0) rscale[m] = ldexpf(1.f, -e);
+  for_row_chunks(xr, K, live, v, [&](int k, float4 c) {
     _Float16 h[4], l[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      h[i] = static_cast<_Float16>(a[i]);
-      l[i] = static_cast<_Float16>(a[i] - static_cast<float>(h[i]));
-    }
+    split4(c, e, h, l);
     const int g = k >> 6, kk = k & 63, t = (kk >> 3) & 1, half = (kk >> 2) & 1;
     const int lane = (kk >> 4) * 16 + (m & 15);
     // uint2 index: 16-byte fragment (g, rt, u, lane) holds two uint2; `half` picks one.
     const size_t frag = ((static_cast<size_t>(g) * RT + rt) * 4 + 2 * t) * kWave + lane;
     xp[frag * 2 + half] = *reinterpret_cast<const uint2*>(h);
     xp[(frag + kWave) * 2 + half] = *reinterpret_cast<const uint2*>(l);
-  }
+  });
 }
 
 template <int RT, int T, int W>
@@ -1406,7 +1443,7 @@ hipError_t launch_tile(const float* x, const int8_t* w, const float* s, float* y
   float* rsc = reinterpret_cast<float*>(base);
   base += align256(static_cast<size_t>(16 * RT) * sizeof(float));
   float* part = reinterpret_cast<float*>(base);
-  hipLaunchKernelGGL(pack_x_kernel, dim3(16 * RT), dim3(kThreads), 0, st, x,
+  hipLaunchKernelGGL(pack_x_kernel, dim3(16 * RT), dim3(kSplitThreads), 0, st, x,
                      reinterpret_cast<uint2*>(xp), rsc, M, K, RT);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -1499,7 +1536,7 @@ hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y
   base += align256(static_cast<size_t>(M) * sizeof(float));
   float* part = p.splits > 1 ? reinterpret_cast<float*>(base) : y;
 
-  hipLaunchKernelGGL(split_x_kernel, dim3(M), dim3(kThreads), 0, st, x, xh, xl, rsc, K);
+  hipLaunchKernelGGL(split_x_kernel, dim3(M), dim3(kSplitThreads), 0, st, x, xh, xl, rsc, K);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (p.cfg == 1)
