@@ -21,6 +21,7 @@ constexpr int kBlock = 256;
 constexpr int kAttnWaves = SQ8_ATTN_WAVES;  // waves per (row, head) attention workgroup
 constexpr int kAttnChunk = SQ8_ATTN_CHUNK;  // cache positions per wave per load step
 constexpr int kRowU = 2;                   // positions per 16-lane group per step
+constexpr int kAttnTableCap = 4096;        // block-table entries staged in LDS by the row kernel
 
 hipStream_t stream_of(void* s) { return static_cast<hipStream_t>(s); }
 int launched() { return hipGetLastError() == hipSuccess ? SQ8_OK : SQ8_ERR_LAUNCH; }
@@ -219,10 +220,11 @@ __device__ __forceinline__ float row16_sum(float v) {
 // head. Each 16-lane group of a wave owns one cache position at a time and lane li of the group
 // holds head dims DPL*li .. +DPL-1 (one coalesced 16*DPL-float row per group and load); a wave
 // steps over kRowStep positions (kRowU per group), the next step's rows in flight while one is
-// used. A score is a 16-lane DPP sum; the running max is updated once per step and head (the
-// wave's maximum over the step), so each (position, head) costs DPL FMAs, 4 DPP adds and one
-// exponential. Groups accumulate their own positions' weighted values under the wave's common
-// running max; groups, then waves, are combined at the end.
+// used. A score is a 16-lane DPP sum; each 16-lane group keeps its own running max per head,
+// updated once per step from the group's U scores, so a (position, head) costs DPL FMAs, 4 DPP
+// adds and one exponential and a step needs no cross-group exchange (a wave-wide max per step,
+// through two lane permutes per head, made every step wait on the permute latency). Groups are
+// brought to a common max and summed at the end, then the waves are combined.
 template <int DPL, int GMAX, int W>
 __global__ __launch_bounds__(W * kWave) void paged_attention_rows_kernel(
     const float* __restrict__ qkv, int q_stride, int head_num, int kv_head_num, int head_size,
@@ -235,11 +237,19 @@ __global__ __launch_bounds__(W * kWave) void paged_attention_rows_kernel(
   constexpr int NV = DPL / 4;  // float4 per lane per cache row
   __shared__ float s_m[W][GMAX], s_l[W][GMAX];
   __shared__ float s_acc[W][GMAX][HS];
+  __shared__ int32_t table[kAttnTableCap];  // the row's block table (table_stride <= cap)
   const int G = head_num / kv_head_num;
   const int r = blockIdx.x / kv_head_num, kvh = blockIdx.x % kv_head_num;
   const int seq = positions[r] + 1;
   const int kv_dim = kv_head_num * HS, hoff = kvh * HS;
-  const int32_t* table = block_table + static_cast<size_t>(r) * table_stride;
+  // Stage the row's block table once: every cache-row address then costs an LDS read instead of
+  // a dependent global load ahead of each step's key/value loads.
+  {
+    const int32_t* gt = block_table + static_cast<size_t>(r) * table_stride;
+    const int nb = (seq + block_size - 1) / block_size;
+    for (int i = threadIdx.x; i < nb; i += W * kWave) table[i] = gt[i];
+    __syncthreads();
+  }
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = lane >> 4, li = lane & 15;
@@ -298,16 +308,17 @@ __global__ __launch_bounds__(W * kWave) void paged_attention_rows_kernel(
         s[u] = posn(c, u) < seq ? sum : -INFINITY;
         mx = fmaxf(mx, s[u]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-      const float mn = fmaxf(m[g], mx);  // finite: the step's first position is < seq
-      const float f = expf(m[g] - mn);
+      // Each 16-lane group keeps its own running max (no cross-group exchange per step); a
+      // group whose positions so far are all past the sequence end still has max -inf.
+      const float mn = fmaxf(m[g], mx);
+      const bool none = mn == -INFINITY;
+      const float f = none ? 1.f : expf(m[g] - mn);
       l[g] *= f;
 #pragma unroll
       for (int j = 0; j < DPL; ++j) acc[g][j] *= f;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const float p = expf(s[u] - mn);
+        const float p = none ? 0.f : expf(s[u] - mn);
         l[g] += p;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
@@ -328,10 +339,17 @@ __global__ __launch_bounds__(W * kWave) void paged_attention_rows_kernel(
     step(1, c + 1);
   }
 
-  // Sum the 4 groups (same running max), then combine the waves.
+  // Bring the 4 groups to the wave's max and sum them, then combine the waves.
 #pragma unroll
   for (int g = 0; g < GMAX; ++g) {
     if (g >= G) break;
+    float mw = fmaxf(m[g], __shfl_xor(m[g], 16, kWave));
+    mw = fmaxf(mw, __shfl_xor(mw, 32, kWave));
+    const float gscale = m[g] == -INFINITY ? 0.f : expf(m[g] - mw);
+    m[g] = mw;
+    l[g] *= gscale;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[g][j] *= gscale;
     float lt = l[g];
     lt += __shfl_xor(lt, 16, kWave);
     lt += __shfl_xor(lt, 32, kWave);
@@ -474,7 +492,7 @@ int sq8_paged_attention(const float* qkv, int q_stride, int rows, int head_num, 
   const int G = head_num / kv_head_num;
   const bool k16 = reinterpret_cast<uintptr_t>(key_cache) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(value_cache) % 16 == 0;
-  if ((head_size == 128 || head_size == 64) && G <= 8 && k16 &&
+  if ((head_size == 128 || head_size == 64) && G <= 8 && k16 && table_stride <= kAttnTableCap &&
       static_cast<int64_t>(rows) * kv_head_num <= 0x7fffffff) {
     // Few workgroups (few, typically long, rows): 8 waves each to keep more rows in flight.
     const bool wide = static_cast<int64_t>(rows) * kv_head_num < 2 * cu_count();
