@@ -458,6 +458,9 @@ namespace {
 
 // LDS bytes the stream kernel may use for staged token rows (MT * K fp32).
 constexpr size_t kStreamLdsMax = 64 * 1024;
+// Two token rows of long K (down projections) may stage up to 128 KiB: fewer workgroups per CU,
+// but the sweep still streams at the single-row rate, against half that for the rows kernel.
+constexpr size_t kStreamLdsTwoRows = 128 * 1024;
 
 // WV waves per workgroup; 16 waves per CU in total, fewer when there are fewer row blocks.
 template <int R, int U, int MT, int GS, int WV, int PRO>
@@ -466,6 +469,20 @@ hipError_t launch_sweep_t(const float* x, const int8_t* w, const float* s, float
   const size_t lds = static_cast<size_t>(MT) * K * sizeof(float);
   const int nblk = (N + R - 1) / R;
   const int grid = min((nblk + WV - 1) / WV, (16 / WV) * cu_count());
+  if (lds > 64 * 1024) {  // above 64 KiB the dynamic LDS size needs the opt-in attribute
+    static bool attr_set = false;
+    if (!attr_set) {
+      const void* kernels[] = {
+          reinterpret_cast<const void*>(sweep_kernel<R, U, MT, GS, false, WV, PRO>),
+          reinterpret_cast<const void*>(sweep_kernel<R, U, MT, GS, true, WV, PRO>)};
+      for (const void* k : kernels) {
+        const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 static_cast<int>(kStreamLdsTwoRows));
+        if (e != hipSuccess) return e;
+      }
+      attr_set = true;
+    }
+  }
   if (K % (1024 * U) == 0) {
     hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, false, WV, PRO>), dim3(grid), dim3(WV * kWave),
                        lds, st, x, w, s, y, M, N, K, gs, pro);
@@ -548,7 +565,8 @@ hipError_t launch_stream(const float* x, const int8_t* w, const float* s, float*
 // Token rows are staged padded to 1, 2 or 4.
 bool gemv_stream_fits(int M, int K) {
   const int mt = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
-  return M <= 4 && static_cast<size_t>(mt) * K * sizeof(float) <= kStreamLdsMax;
+  const size_t cap = mt == 2 ? kStreamLdsTwoRows : kStreamLdsMax;
+  return M <= 4 && static_cast<size_t>(mt) * K * sizeof(float) <= cap;
 }
 
 // Requires: group_size % 16 == 0, K % group_size == 0, 16-byte aligned x and w.

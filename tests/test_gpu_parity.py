@@ -54,10 +54,12 @@ def test_small_shapes(sq8, dev, M, N, K):
 
 @pytest.mark.parametrize("M", [1, 2, 4])
 @pytest.mark.parametrize("N,K,gs", [(33, 8192, 64), (50, 9280, 64), (17, 14336, 64),
-                                    (9, 14336, 32), (21, 16000, 64), (300, 7168, 64)])
+                                    (9, 14336, 32), (21, 16000, 64), (300, 7168, 64),
+                                    (19, 20480, 64)])
 def test_long_rows_decode(sq8, dev, M, N, K, gs):
-    """Decode rows of 7-16 K elements: one-row-per-wave configurations, with and without a
-    partial last step, and rows whose staged activations exceed the LDS budget at M=2."""
+    """Decode rows of 7-20 K elements: one-row-per-wave configurations, with and without a
+    partial last step, two token rows staged in up to 128 KiB of LDS, and rows whose staged
+    activations exceed even that at M=2 (20480: the rows kernel)."""
     x, q, s = o.make_case(M, N, K, gs, seed=K + N + M)
     print(f"case M={M} N={N} K={K} gs={gs} path={sq8.path_name(M, N, K, gs)}", flush=True)
     check(run(sq8, dev, x, q, s, gs), o.matmul_f64(x, q, s, gs), f"M={M} N={N} K={K} gs={gs}")
