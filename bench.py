@@ -180,7 +180,9 @@ def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed:
     lognormal with median 200 (sigma 0.8, clipped to 16..2048), uniform random token ids,
     n_new greedy tokens each, paged KV with block size 16 (the reference's choice for a mean
     prompt of 64..1024), at most 64 running sequences and 64 rows per step (the reference's
-    max_batch). Eager launches; every step syncs once for its greedy tokens."""
+    max_batch). Decode-only steps replay a HIP graph per row count (captured before timing, as
+    a server captures at start-up); steps with prefill rows launch eagerly; every step syncs once
+    for its greedy tokens."""
     import importlib
     import numpy as np
     mf = importlib.import_module("llm_steadyinfer_amd.model_file")
@@ -203,6 +205,8 @@ def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed:
                       block_size=block)
     model = bm.PagedBatchModel(cfg, w, GS, max_rows=64, max_seq_len=max_seq,
                                num_blocks=s.alloc.num_blocks, block_size=block, device=dev)
+    # Decode-step graphs for every row count, captured at start-up (not timed).
+    capture_s = model.capture_decode_graphs()
     s.forward = model.forward
     for p in ([5, 6, 7], [8, 9]):          # warm-up requests (every kernel once), not timed
         s.add_request(p)
@@ -229,7 +233,9 @@ def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed:
             "rows": s.rows_run - rows0, "preemptions": s.preemptions,
             "kv_pool_GB": round(2 * 4 * cfg.layer_num * cfg.kv_dim * block * s.alloc.num_blocks
                                 / 1e9, 2),
-            "launch": "eager, one host sync per step"}
+            "graph_replays": model.graph_replays, "graph_capture_s": round(capture_s, 2),
+            "launch": "decode-only steps: one HIP graph per row count (captured at start-up); "
+                      "steps with prefill rows: eager; one host sync per step"}
 
 def main():
     ap = argparse.ArgumentParser()

@@ -16,7 +16,14 @@ followed by a plain RMSNorm) and the SwiGLU in the gate/up matmul's, as
 sq8_matmul_epilogue does.
 
 All rows write their KV before any row attends, so prefill rows of one sequence in the same step
-see each other causally. The KV pool is [layers][num_blocks][block_size][kv_dim] fp32 for keys
+see each other causally.
+
+A decode-only step (every row a decode row) launches the same kernels for the same row count B
+every time: its inputs (tokens, positions, block tables) live in fixed device buffers. The first
+such step at each B runs eagerly and then captures the launch sequence into a HIP graph; later
+decode-only steps at that B replay it (one launch instead of ~15 per layer), the way the
+reference captures its decode steps (src/source/model/model.cpp:189-238). The matmul workspace is
+sized for every row count up front, so no later step can move a buffer a graph points to. The KV pool is [layers][num_blocks][block_size][kv_dim] fp32 for keys
 and for values (KVManager's paged layout, src/source/scheduler/kv_manager.cpp).
 """
 from __future__ import annotations
@@ -25,16 +32,16 @@ from typing import List
 
 import numpy as np
 
-from . import (SQ8_EPI_RESIDUAL, SQ8_EPI_SWIGLU, Workspace, add_rmsnorm, argmax_rows, embedding,
-               epilogue_fused, matmul, matmul_epilogue, paged_attention, paged_rope_kv, rmsnorm,
-               rope_tables, swiglu_rows)
+from . import (SQ8_EPI_NONE, SQ8_EPI_RESIDUAL, SQ8_EPI_SWIGLU, Workspace, add_rmsnorm,
+               argmax_rows, embedding, epilogue_fused, lib, matmul, matmul_epilogue,
+               paged_attention, paged_rope_kv, rmsnorm, rope_tables, swiglu_rows)
 
 EPS = 1e-6
 
 
 class PagedBatchModel:
     def __init__(self, cfg, weights: dict, group_size: int, max_rows: int, max_seq_len: int,
-                 num_blocks: int, block_size: int, device="cuda"):
+                 num_blocks: int, block_size: int, device="cuda", use_graphs: bool = True):
         import torch
         self.torch = torch
         self.cfg, self.w, self.gs = cfg, weights, group_size
@@ -65,13 +72,24 @@ class PagedBatchModel:
         self.ws = Workspace(device)
         self.rows_run = 0
         self._fuse = {}
+        self.use_graphs = use_graphs
+        self.graphs = {}
+        self.graph_replays = 0
+        # Workspace for every row count and projection, allocated once (graphs keep its address).
+        need = 0
+        for B in range(1, R + 1):
+            for (N, K) in ((d + 2 * kv, d), (d, d), (2 * h, d), (d, h), (cfg.vocab, d)):
+                for epi in (SQ8_EPI_NONE, SQ8_EPI_RESIDUAL, SQ8_EPI_SWIGLU):
+                    need = max(need, int(lib().sq8_epilogue_workspace_bytes(B, N, K, group_size,
+                                                                            epi)))
+        self.ws.get(need)
 
     @classmethod
     def from_decoder(cls, dec, max_rows: int, max_seq_len: int, num_blocks: int,
-                     block_size: int) -> "PagedBatchModel":
+                     block_size: int, use_graphs: bool = True) -> "PagedBatchModel":
         """Share the fused weights of an Int8Decoder (model file or random init)."""
         return cls(dec.cfg, dec.w, dec.gs, max_rows, max_seq_len, num_blocks, block_size,
-                   dec.device)
+                   dec.device, use_graphs=use_graphs)
 
     def kv_bytes_per_position(self) -> int:
         return 2 * 4 * self.cfg.layer_num * self.cfg.kv_dim
@@ -111,11 +129,49 @@ class PagedBatchModel:
         self.pos[:B].copy_(torch.from_numpy(pos))
         self.table[:B].copy_(torch.from_numpy(tab))
         stream = torch.cuda.current_stream()
-        self.launch(B, nd, stream)
+        graph = self.graphs.get(B) if self.use_graphs and nd == B else None
+        if graph is not None:
+            graph.replay()
+            self.graph_replays += 1
+        else:
+            self.launch(B, nd, stream)
+            if self.use_graphs and nd == B:
+                self._capture(B)
         self.rows_run += B
         if nd == 0:
             return []
         return self.next[:nd].cpu().tolist()
+
+    def capture_decode_graphs(self, rows=None) -> float:
+        """Capture the decode-only step graphs for the given row counts (default 1..max_rows) up
+        front, as a server does at start-up, instead of at the first decode-only step of each
+        row count. Each capture follows one eager run on placeholder rows (token 0 at position 0
+        of physical block 0), so call this before any sequence holds cache blocks. Returns the
+        seconds spent."""
+        import time
+        torch = self.torch
+        t0 = time.perf_counter()
+        for B in (rows if rows is not None else range(1, self.max_rows + 1)):
+            if B in self.graphs:
+                continue
+            self.tok[:B].zero_()
+            self.pos[:B].zero_()
+            self.table[:B].zero_()
+            self.launch(B, B, torch.cuda.current_stream())
+            self._capture(B)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0
+
+    def _capture(self, B: int) -> None:
+        """Capture the decode-only step at B rows (after one eager run at B)."""
+        torch = self.torch
+        s = torch.cuda.Stream(device=self.x.device)
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            self.launch(B, B, s)
+        torch.cuda.current_stream().wait_stream(s)
+        self.graphs[B] = g
 
     def launch(self, B: int, nd: int, stream) -> None:
         """Enqueue the forward of the first B staged rows (tokens, positions and block tables in

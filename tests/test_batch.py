@@ -147,12 +147,15 @@ def test_swiglu_and_argmax_rows(sq8, dev):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("max_batch,block_size,num_blocks", [(4, 4, None), (4, 4, 20), (4, 4, 24),
-                                                           (8, 8, None), (96, 8, None)])
-def test_continuous_batching_matches_oracle(dev, tmp_path, max_batch, block_size, num_blocks):
+@pytest.mark.parametrize("max_batch,block_size,num_blocks,graphs", [
+    (4, 4, None, True), (4, 4, 20, True), (4, 4, 24, True), (8, 8, None, True),
+    (96, 8, None, True), (8, 8, None, False)])
+def test_continuous_batching_matches_oracle(dev, tmp_path, max_batch, block_size, num_blocks,
+                                            graphs):
     """Six prompts (1..40 tokens) scheduled with chunked prefill mixed into decode steps (and,
     with a 20- or 24-block pool, preemption and recompute): every sequence's greedy tokens equal the
-    float64 oracle decoding it alone."""
+    float64 oracle decoding it alone. Decode-only steps replay per-row-count HIP graphs between
+    eager prefill steps (and run eagerly in the graphs=False case)."""
     sched = importlib.import_module("llm_steadyinfer_amd.scheduler")
     bm = importlib.import_module("llm_steadyinfer_amd.batch_model")
     dec = importlib.import_module("llm_steadyinfer_amd.decoder")
@@ -166,13 +169,16 @@ def test_continuous_batching_matches_oracle(dev, tmp_path, max_batch, block_size
     s = sched.Scheduler(None, max_batch=max_batch, max_seq_len=max_seq, max_gen_len=n_new,
                         block_size=block_size, num_blocks=num_blocks)
     model = bm.PagedBatchModel.from_decoder(D, max_rows=max_batch, max_seq_len=max_seq,
-                                            num_blocks=s.alloc.num_blocks, block_size=block_size)
+                                            num_blocks=s.alloc.num_blocks, block_size=block_size,
+                                            use_graphs=graphs)
     s.forward = model.forward
     for p in prompts:
         assert s.add_request(p) >= 0
     done = s.run(max_steps=5000)
     got = [q.generated_tokens for q in done]
-    print("steps", s.steps, "rows", s.rows_run, "preemptions", s.preemptions)
+    print("steps", s.steps, "rows", s.rows_run, "preemptions", s.preemptions,
+          "graph replays", model.graph_replays, "graphs", sorted(model.graphs))
+    assert (model.graph_replays > 0) == graphs
     if num_blocks is not None:
         assert s.preemptions > 0
     if max_batch > 64:  # the 88 prompt tokens start as one step: the fused-epilogue GEMM path
