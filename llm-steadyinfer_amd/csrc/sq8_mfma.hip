@@ -1238,6 +1238,200 @@ __global__ __launch_bounds__(W * kWave) void tile_kernel(
     __hip_atomic_store(&tickets[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---------------------------------------------------------------- decode GEMM (9..64 rows)
+// A workgroup of W waves owns 16*T*W output columns and a range of K groups (its split); each
+// wave owns 16*T of the columns for all 16*RT token rows. Per 64-wide group:
+//  * the activation fragments of the group (pack_x_kernel's MFMA-ready layout, RT*4 KiB) arrive
+//    in an S-stage LDS ring by global -> LDS DMA, once per workgroup, and every wave reads them
+//    from there (the tile kernel loads them per wave from L2, 4x the weight bytes);
+//  * the wave's weights (16 bytes per lane and column tile, v_mfma_f32_16x16x32_f16 B layout) go
+//    straight into a D-deep register ring. Under full load the memory latency is several
+//    microseconds, and streaming HBM at full rate needs ~128 KiB in flight per CU:
+//    D = 8 groups x 8 waves x 2 tiles x 1 KiB;
+//  * the split's scales are staged in LDS once, up front, with row-contiguous loads.
+// The DMA is issued from inline asm. Each thread issues the same loads per group: the DMA and
+// then the weights of the group D-1 ahead (one distance for both: a wait counter drains in order,
+// so waiting for a DMA issued closer than the weights would also drain weights meant to stay in
+// flight). It waits until the group's DMA and weights have landed, and a barrier publishes the
+// stage and frees the one refilled next. Groups past the split re-read its last group with scale
+// 0, so every step issues its loads unconditionally.
+template <int RT, int T, int W, int D>
+__global__ __launch_bounds__(W * kWave) void dgemm_kernel(
+    const u32x4* xp, const float* __restrict__ rscale, const int8_t* w, const float* s,
+    float* out, int M, int N, int K, int gs, int gps, Epi epi) {
+  constexpr int XSTAGE = RT * 4 * kWave * 16;          // bytes of one group's fragments
+  constexpr int NCH = XSTAGE / (kWave * 16);           // 1 KiB chunks of a group's fragments
+  constexpr int LXD = (NCH + W - 1) / W;               // DMA instructions per thread per group
+  static_assert(T % 2 == 0, "SwiGLU pairs tile j with tile j + T/2");
+  constexpr int LOADS = LXD + T;                       // loads per thread per group
+  constexpr int WAIT = (D - 2) * LOADS;                // see the step order below
+  static_assert(D >= 2 && WAIT < 64, "ring depth");
+  constexpr int HT = T / 2;
+  constexpr int COLS = 16 * T * W;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lcol = lane & 15, kq = (lane >> 4) * 16;
+  const int G = K / BK, gpr = K / gs;
+  const int gsplit = blockIdx.y * gps;
+  const int gcount = min(G, gsplit + gps) - gsplit;
+  const int sstride = gcount + 1;                      // padded: no bank conflicts across lcol
+  const bool swiglu = epi.mode == kEpiSwiglu;
+  const int F = N / 2;
+  const int n0 = blockIdx.x * COLS, f0 = blockIdx.x * (COLS / 2);
+  // Weight row of workgroup column c = (wv * T + j) * 16 + l (SwiGLU: tiles j < T/2 hold the gate
+  // rows of the wave's features, tiles j >= T/2 the matching up rows).
+  auto wrow = [&](int c) __attribute__((always_inline)) {
+    if (!swiglu) return min(n0 + c, N - 1);
+    const int wv = c / (16 * T), j = (c / 16) % T, l = c % 16;
+    const int f = f0 + (wv * HT + j % HT) * 16 + l;
+    return min(f, F - 1) + (j >= HT ? F : 0);
+  };
+  float* sscale = reinterpret_cast<float*>(smem + D * XSTAGE);
+  for (int idx = tid; idx < COLS * gcount; idx += W * kWave) {
+    const int c = idx / gcount, gi = idx - c * gcount;
+    sscale[c * sstride + gi] = s[static_cast<size_t>(wrow(c)) * gpr + ((gsplit + gi) * BK) / gs];
+  }
+  const int8_t* wr[T];
+#pragma unroll
+  for (int j = 0; j < T; ++j)
+    wr[j] = w + static_cast<size_t>(wrow((wave * T + j) * 16 + lcol)) * K + kq;
+  const float* scol[T];
+#pragma unroll
+  for (int j = 0; j < T; ++j) scol[j] = sscale + ((wave * T + j) * 16 + lcol) * sstride;
+
+  const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
+  const int nsteps = gcount;
+  auto gclamp = [&](int i) { return gsplit + min(i, nsteps - 1); };
+  auto dma_x = [&](int i, int slot) __attribute__((always_inline)) {
+    const char* src = reinterpret_cast<const char*>(xp) + static_cast<size_t>(gclamp(i)) * XSTAGE;
+    // Every wave issues LXD copies; when the chunks do not divide evenly, the surplus ones copy
+    // a chunk again (same bytes to the same place), so all waves count the same loads.
+#pragma unroll
+    for (int q = 0; q < LXD; ++q) {
+      const uint32_t off = static_cast<uint32_t>(((q * W + wave) % NCH) * kWave * 16);
+      dma16(src, off + lane * 16u, lds0 + slot * XSTAGE + off);
+    }
+  };
+  // Weight loads from inline asm too: the compiler does not count them, so it inserts no wait
+  // of its own; tie() after the wait below keeps every use of a ring slot behind that wait.
+  u32x4 wq[D][T];
+  auto load_w = [&](int i, int slot) __attribute__((always_inline)) {
+    const int g = gclamp(i);
+#pragma unroll
+    for (int j = 0; j < T; ++j)
+      asm volatile("global_load_dwordx4 %0, %1, off nt"
+                   : "=v"(wq[slot][j])
+                   : "v"(wr[j] + static_cast<size_t>(g) * BK)
+                   : "memory");
+  };
+  auto tie = [&](int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < T; ++j) asm volatile("" : "+v"(wq[slot][j]));
+  };
+
+  f4v acc[RT][T];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int j = 0; j < T; ++j) acc[r][j] = f4v{0.f, 0.f, 0.f, 0.f};
+
+  // Prologue: DMA and weights for groups 0 .. D-2 (the scale stage's loads were consumed by its
+  // LDS writes above, so they are not outstanding).
+#pragma unroll
+  for (int p = 0; p < D - 1; ++p) {
+    dma_x(p, p);
+    load_w(p, p);
+  }
+  const int nloop = (nsteps + D - 1) / D * D;
+  for (int i0 = 0; i0 < nloop; i0 += D) {
+#pragma unroll
+    for (int b = 0; b < D; ++b) {
+      const int i = i0 + b;
+      wait_vmcnt<WAIT>();  // group i's DMA and weights (issued D-1 groups ago) have landed
+      tie(b);
+      __syncthreads();  // publishes stage i (and, the first time, the scale stage)
+      asm volatile("" ::: "memory");
+      dma_x(i + D - 1, (b + D - 1) % D);
+      load_w(i + D - 1, (b + D - 1) % D);
+      asm volatile("" ::: "memory");
+      const char* xs = smem + b * XSTAGE;
+      const bool live = i < nsteps;
+      h8 bw[T][2];
+      float sc[T];
+#pragma unroll
+      for (int j = 0; j < T; ++j) {
+        uint32_t hq[8];
+        i8x4_to_h4(wq[b][j].x, hq[0], hq[1]);
+        i8x4_to_h4(wq[b][j].y, hq[2], hq[3]);
+        i8x4_to_h4(wq[b][j].z, hq[4], hq[5]);
+        i8x4_to_h4(wq[b][j].w, hq[6], hq[7]);
+        const u32x4 b0 = {hq[0], hq[1], hq[2], hq[3]};
+        const u32x4 b1 = {hq[4], hq[5], hq[6], hq[7]};
+        bw[j][0] = __builtin_bit_cast(h8, b0);
+        bw[j][1] = __builtin_bit_cast(h8, b1);
+        sc[j] = live ? scol[j][min(i, nsteps - 1)] : 0.f;
+      }
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        // one row tile's fragments at a time (hoisting all of them spills at RT >= 3)
+        if (RT >= 3) __builtin_amdgcn_sched_barrier(0);
+        h8 a[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          a[u] = *reinterpret_cast<const h8*>(xs + ((r * 4 + u) * kWave + lane) * 16);
+#pragma unroll
+        for (int j = 0; j < T; ++j) {
+          const f4v zero = {0.f, 0.f, 0.f, 0.f};
+          f4v pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0], bw[j][0], zero, 0, 0, 0);
+          pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1], bw[j][0], pr, 0, 0, 0);
+          pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[2], bw[j][1], pr, 0, 0, 0);
+          pr = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[3], bw[j][1], pr, 0, 0, 0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[r][j][e] = fmaf(sc[j], pr[e], acc[r][j][e]);
+        }
+      }
+    }
+  }
+  wait_vmcnt<0>();  // the clamped tail loads land before the workgroup ends
+
+  // Output: acc[r][j][e] is row 16 r + 4 (lane / 16) + e, column lcol of tile j.
+  const bool partial = gridDim.y > 1;
+  float* dst = out + (partial ? static_cast<size_t>(blockIdx.y) * M * N : 0);
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = 16 * r + 4 * (lane >> 4) + e;
+      if (m >= M) continue;
+      const float rsc = rscale[m];
+      if (swiglu) {
+#pragma unroll
+        for (int j = 0; j < HT; ++j) {
+          const int f = f0 + (wave * HT + j) * 16 + lcol;
+          if (f >= F) continue;
+          const float g = acc[r][j][e] * rsc, u = acc[r][j + HT][e] * rsc;
+          if (partial) {
+            dst[static_cast<size_t>(m) * N + f] = g;
+            dst[static_cast<size_t>(m) * N + F + f] = u;
+          } else {
+            dst[static_cast<size_t>(m) * F + f] = silu_mul(g, u);
+          }
+        }
+        continue;
+      }
+#pragma unroll
+      for (int j = 0; j < T; ++j) {
+        const int n = n0 + (wave * T + j) * 16 + lcol;
+        if (n >= N) continue;
+        const size_t o = static_cast<size_t>(m) * N + n;
+        const float v = acc[r][j][e] * rsc;
+        dst[o] = !partial && epi.mode == kEpiResidual ? epi.res[o] + v : v;
+      }
+    }
+  }
+}
+
 // Sum split-K partials in split order, y[i] = sum_z part[z][i], then apply the epilogue:
 // residual: y[i] = res[i] + sum; SwiGLU (part holds M rows of N = 2F): y[m][f] =
 // silu(gate sum) * (up sum).
@@ -1285,11 +1479,19 @@ __global__ __launch_bounds__(kThreads) void epilogue_kernel(const float* __restr
 
 size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 
+// Decode GEMM configuration: 4 waves x 4 column tiles of 16, an 8-deep weight ring, 4 LDS stages.
+constexpr int kDgT = 2, kDgW = 8, kDgDepth = 8;
+// Ring depth for RT row tiles: 4 tiles take 16 KiB of LDS per group, so their ring is shorter.
+constexpr int dg_depth(int rt) { return rt >= 3 ? 4 : kDgDepth; }
+constexpr int kDgCols = 16 * kDgT * kDgW;
+constexpr int kDgScaleGroups = 32;  // groups per split at most (the LDS scale stage)
+
 // Largest M served by the single-launch skinny kernel.
 constexpr int kSkinnyMaxM = 32;
 
 struct Plan {
   bool tile;      // pack_x_kernel + tile_kernel (9 <= M <= 64)
+  bool dgemm;     // pack_x_kernel + dgemm_kernel (+ splitk_reduce_kernel); uses rt
   int rt, tn, tw; // tile: 16-row activation tiles, 16-column tiles per wave, waves per workgroup
   bool skinny;
   int kw;         // skinny: K groups per chunk (divides groups_per_split)
@@ -1310,6 +1512,20 @@ Plan make_plan(int M, int N, int K) {
   // sweeps over the Llama-3-8B projections: wide outputs (N >= 16384) take 4 column tiles per
   // wave and no K split; others take 2 tiles, 8 waves, and split K when the grid has at most
   // 1024 waves.
+  // Decode GEMM for wide outputs at 33-64 tokens (Llama gate/up at 48 and 64 rows: 59 and 63 us
+  // against 70 and 77 for the tile kernel, which stays ahead on narrower outputs, where the
+  // decode GEMM needs a deep K split to fill the GPU).
+  if (M > 32 && M <= 64 && N >= 16384) {
+    p.dgemm = true;
+    p.rt = rt;
+    const int tiles = (N + kDgCols - 1) / kDgCols;
+    const int want = std::max(1, (cu_count() + tiles / 2) / tiles);
+    int gpsplit = (nsteps + want - 1) / want;
+    gpsplit = (gpsplit + kDgDepth - 1) / kDgDepth * kDgDepth;
+    p.groups_per_split = std::min(std::min(gpsplit, nsteps), kDgScaleGroups);
+    p.splits = (nsteps + p.groups_per_split - 1) / p.groups_per_split;
+    return p;
+  }
   if (M > 8 && M <= 64 && !(K >= 8192 && (rt == 1 || rt > 2))) {
     p.tile = true;
     p.rt = rt;
@@ -1433,6 +1649,43 @@ hipError_t launch_skinny_i8(const float* x, const int8_t* w, const float* s, flo
   return hipGetLastError();
 }
 
+template <int RT>
+hipError_t launch_dgemm(const float* x, const int8_t* w, const float* s, float* y, void* ws, int M,
+                        int N, int K, int gs, const Plan& p, hipStream_t st, Epi epi) {
+  char* base = static_cast<char*>(ws) + kTicketBytes;
+  u32x4* xp = reinterpret_cast<u32x4*>(base);
+  base += align256(static_cast<size_t>(K / BK) * RT * 4 * kWave * sizeof(u32x4));
+  float* rsc = reinterpret_cast<float*>(base);
+  base += align256(static_cast<size_t>(16 * RT) * sizeof(float));
+  float* part = reinterpret_cast<float*>(base);
+  hipLaunchKernelGGL(pack_x_kernel, dim3(16 * RT), dim3(kSplitThreads), 0, st, x,
+                     reinterpret_cast<uint2*>(xp), rsc, M, K, RT);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  auto kern = dgemm_kernel<RT, kDgT, kDgW, dg_depth(RT)>;
+  constexpr size_t lds = static_cast<size_t>(dg_depth(RT)) * RT * 4 * kWave * 16 +
+                        static_cast<size_t>(kDgCols) * (kDgScaleGroups + 1) * sizeof(float);
+  static bool attr_set = false;
+  if (!attr_set && lds > 64 * 1024) {
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const int cols = epi.mode == kEpiSwiglu ? (N / 2 + kDgCols / 2 - 1) / (kDgCols / 2)
+                                          : (N + kDgCols - 1) / kDgCols;
+  float* out = p.splits > 1 ? part : y;
+  hipLaunchKernelGGL(kern, dim3(cols, p.splits), dim3(kDgW * kWave), lds, st, xp, rsc, w, s,
+                     out, M, N, K, gs, p.groups_per_split, epi);
+  e = hipGetLastError();
+  if (e != hipSuccess || p.splits == 1) return e;
+  const size_t count = static_cast<size_t>(M) * (epi.mode == kEpiSwiglu ? N / 2 : N);
+  const int grid = static_cast<int>(std::min<size_t>((count + kThreads - 1) / kThreads, 4096));
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid), dim3(kThreads), 0, st, part, y, M, N,
+                     p.splits, epi);
+  return hipGetLastError();
+}
+
 template <int RT, int T, int W>
 hipError_t launch_tile(const float* x, const int8_t* w, const float* s, float* y, void* ws, int M,
                        int N, int K, int gs, const Plan& p, hipStream_t st) {
@@ -1460,7 +1713,7 @@ hipError_t launch_tile(const float* x, const int8_t* w, const float* s, float* y
 size_t mfma_workspace_bytes(int M, int N, int K) {
   const Plan p = make_plan(M, N, K);
   size_t b = kTicketBytes;
-  if (p.tile) {
+  if (p.tile || p.dgemm) {
     b += align256(static_cast<size_t>(K / BK) * p.rt * 4 * kWave * sizeof(u32x4));
     b += align256(static_cast<size_t>(16 * p.rt) * sizeof(float));
   } else if (!p.skinny) {
@@ -1475,7 +1728,7 @@ size_t mfma_workspace_bytes(int M, int N, int K) {
 // workspace of mfma_workspace_bytes(M, N, K).
 bool mfma_fuses_epilogue(int M, int N, int K) {
   const Plan p = make_plan(M, N, K);
-  return !p.tile && !p.skinny;
+  return !p.tile && !p.skinny;  // the GEMM and the decode GEMM
 }
 
 hipError_t launch_epilogue(const float* t, float* y, int M, int N, Epi epi, hipStream_t st) {
@@ -1489,6 +1742,14 @@ hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y
                        int K, int gs, void* ws, hipStream_t st, Epi epi) {
   const Plan p = make_plan(M, N, K);
   if (epi.mode != kEpiNone && (p.tile || p.skinny)) return hipErrorInvalidValue;
+  if (p.dgemm) {
+    switch (p.rt) {
+      case 1: return launch_dgemm<1>(x, w, s, y, ws, M, N, K, gs, p, st, epi);
+      case 2: return launch_dgemm<2>(x, w, s, y, ws, M, N, K, gs, p, st, epi);
+      case 3: return launch_dgemm<3>(x, w, s, y, ws, M, N, K, gs, p, st, epi);
+      default: return launch_dgemm<4>(x, w, s, y, ws, M, N, K, gs, p, st, epi);
+    }
+  }
   unsigned* tickets = static_cast<unsigned*>(ws);
   char* base = static_cast<char*>(ws) + kTicketBytes;
   if (p.tile) {

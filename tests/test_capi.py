@@ -108,6 +108,8 @@ def test_epilogue_fusion_and_workspace(sq8):
     assert sq8.epilogue_fused(64, 4096, 14336)
     assert not sq8.epilogue_fused(1, 28672, 4096)
     assert not sq8.epilogue_fused(16, 28672, 4096)
+    assert sq8.epilogue_fused(48, 28672, 4096)      # the decode GEMM (wide outputs, 33-64 rows)
+    assert not sq8.epilogue_fused(48, 6144, 4096)   # the tile kernel
     L = sq8.lib()
     for M, N, K in ((1, 8192, 4096), (16, 8192, 4096), (2048, 8192, 4096)):
         base = sq8.workspace_bytes(M, N, K, 64)

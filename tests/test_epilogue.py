@@ -34,10 +34,11 @@ def to_dev(dev, *arrs):
 
 
 # (M, F, K): the GEMM path with one split and with split-K (few tiles), features not a multiple
-# of the 128-feature workgroup, and the decode paths (GEMV, skinny, tile) that apply the epilogue
-# after the product.
+# of the 128-feature workgroup, the decode paths (GEMV, skinny, tile) that apply the epilogue
+# after the product, and the decode GEMM (33-64 rows, wide outputs), which fuses it.
 SWIGLU_CASES = [(65, 256, 1024), (128, 200, 4096), (300, 512, 256), (2048, 128, 1024),
-                (1, 384, 1024), (4, 160, 2048), (8, 256, 4096), (16, 512, 1024), (33, 96, 8192)]
+                (1, 384, 1024), (4, 160, 2048), (8, 256, 4096), (16, 512, 1024), (33, 96, 8192),
+                (48, 8200, 1024), (64, 8192, 512)]
 
 
 @pytest.mark.parametrize("M,F,K", SWIGLU_CASES)
@@ -62,7 +63,8 @@ def test_swiglu_epilogue(sq8, dev, M, F, K):
 
 
 RESID_CASES = [(65, 512, 1024), (128, 4096, 4096), (300, 1000, 2048), (2048, 256, 1024),
-               (1, 512, 1024), (8, 4096, 4096), (16, 1024, 1024), (40, 4096, 14336)]
+               (1, 512, 1024), (8, 4096, 4096), (16, 1024, 1024), (40, 4096, 14336),
+               (64, 16384, 512), (36, 16400, 1024)]
 
 
 @pytest.mark.parametrize("M,N,K", RESID_CASES)

@@ -209,3 +209,14 @@ def test_gemm_64_row_tiles(sq8, dev, M, N, K, gs):
     x, q, s = o.make_case(M, N, K, gs, seed=M * 11 + N + K)
     print(f"case M={M} N={N} K={K} gs={gs} fused={sq8.epilogue_fused(M, N, K, gs)}", flush=True)
     check(run(sq8, dev, x, q, s, gs), o.matmul_f64(x, q, s, gs), f"M={M} N={N} K={K} gs={gs}")
+
+
+@pytest.mark.parametrize("M,N,K,gs", [(33, 16640, 1024, 64), (40, 16400, 2048, 128),
+                                      (48, 16384, 4096, 64), (64, 17000, 512, 64)])
+def test_decode_gemm_wide_outputs(sq8, dev, M, N, K, gs):
+    """33-64 token rows on wide outputs take the decode GEMM (register weight ring, activation
+    fragments shared through LDS): K split over several workgroups, ragged last column tiles,
+    group size 128, and a split shorter than the ring."""
+    x, q, s = o.make_case(M, N, K, gs, seed=M * 3 + N + K)
+    print(f"case M={M} N={N} K={K} gs={gs} fused={sq8.epilogue_fused(M, N, K, gs)}", flush=True)
+    check(run(sq8, dev, x, q, s, gs), o.matmul_f64(x, q, s, gs), f"M={M} N={N} K={K} gs={gs}")
