@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace sq8 {
 
 constexpr int kWave = 64;  // CDNA wavefront width
@@ -27,6 +29,21 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // Bytes of split-K tickets at the start of every MFMA workspace. They must be zero before the
 // first call and every call leaves them zero, so no other use of a workspace may write there.
 constexpr int kWsTicketBytes = 64 * 1024;
+
+// Opt a kernel in to `bytes` of dynamic LDS (needed above 64 KiB) once per device: `done` holds
+// one bit per device id below 64 (higher ids set the attribute on every call).
+inline hipError_t ensure_dynamic_lds(const void* kernel, size_t bytes,
+                                     std::atomic<uint64_t>& done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = dev >= 0 && dev < 64 ? uint64_t{1} << dev : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          static_cast<int>(bytes));
+  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_release);
+  return e;
+}
 
 // Launchers (host side). Each returns hipSuccess or the launch error.
 hipError_t launch_gemv(const float* x, const int8_t* w, const float* s, float* y, int M, int N,

@@ -470,18 +470,15 @@ hipError_t launch_sweep_t(const float* x, const int8_t* w, const float* s, float
   const int nblk = (N + R - 1) / R;
   const int grid = min((nblk + WV - 1) / WV, (16 / WV) * cu_count());
   if (lds > 64 * 1024) {  // above 64 KiB the dynamic LDS size needs the opt-in attribute
-    static bool attr_set = false;
-    if (!attr_set) {
-      const void* kernels[] = {
-          reinterpret_cast<const void*>(sweep_kernel<R, U, MT, GS, false, WV, PRO>),
-          reinterpret_cast<const void*>(sweep_kernel<R, U, MT, GS, true, WV, PRO>)};
-      for (const void* k : kernels) {
-        const hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 static_cast<int>(kStreamLdsTwoRows));
-        if (e != hipSuccess) return e;
-      }
-      attr_set = true;
-    }
+    static std::atomic<uint64_t> done_full{0}, done_tail{0};
+    hipError_t e = ensure_dynamic_lds(
+        reinterpret_cast<const void*>(sweep_kernel<R, U, MT, GS, false, WV, PRO>),
+        kStreamLdsTwoRows, done_full);
+    if (e == hipSuccess)
+      e = ensure_dynamic_lds(
+          reinterpret_cast<const void*>(sweep_kernel<R, U, MT, GS, true, WV, PRO>),
+          kStreamLdsTwoRows, done_tail);
+    if (e != hipSuccess) return e;
   }
   if (K % (1024 * U) == 0) {
     hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, false, WV, PRO>), dim3(grid), dim3(WV * kWave),

@@ -1599,14 +1599,9 @@ hipError_t launch_gemm(const _Float16* xh, const _Float16* xl, const float* rsc,
                             int gs, const Plan& p, hipStream_t st, Epi epi) {
   using T = PTile<WM, WN, TM, TN, STAGES, GPS>;
   auto kern = gemm_kernel<WM, WN, TM, TN, STAGES, GPS>;
-  static bool attr_set = false;  // LDS above 64 KiB needs the opt-in attribute
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(T::LDS_BYTES));
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> done{0};  // LDS above 64 KiB needs the opt-in attribute
+  hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(kern), T::LDS_BYTES, done);
+  if (e != hipSuccess) return e;
   // SwiGLU: a workgroup owns BN/2 features (their gate and up rows)
   const int cols = epi.mode == kEpiSwiglu ? (N / 2 + T::BN / 2 - 1) / (T::BN / 2)
                                           : (N + T::BN - 1) / T::BN;
@@ -1665,12 +1660,10 @@ hipError_t launch_dgemm(const float* x, const int8_t* w, const float* s, float* 
   auto kern = dgemm_kernel<RT, kDgT, kDgW, dg_depth(RT)>;
   constexpr size_t lds = static_cast<size_t>(dg_depth(RT)) * RT * 4 * kWave * 16 +
                         static_cast<size_t>(kDgCols) * (kDgScaleGroups + 1) * sizeof(float);
-  static bool attr_set = false;
-  if (!attr_set && lds > 64 * 1024) {
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  static std::atomic<uint64_t> done{0};
+  if (lds > 64 * 1024) {
+    e = ensure_dynamic_lds(reinterpret_cast<const void*>(kern), lds, done);
     if (e != hipSuccess) return e;
-    attr_set = true;
   }
   const int cols = epi.mode == kEpiSwiglu ? (N / 2 + kDgCols / 2 - 1) / (kDgCols / 2)
                                           : (N + kDgCols - 1) / kDgCols;
