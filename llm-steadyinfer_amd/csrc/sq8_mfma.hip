@@ -1484,7 +1484,9 @@ constexpr int kDgT = 2, kDgW = 8, kDgDepth = 8;
 // Ring depth for RT row tiles: 4 tiles take 16 KiB of LDS per group, so their ring is shorter.
 constexpr int dg_depth(int rt) { return rt >= 3 ? 4 : kDgDepth; }
 constexpr int kDgCols = 16 * kDgT * kDgW;
-constexpr int kDgScaleGroups = 32;  // groups per split at most (the LDS scale stage)
+// Groups per split at most: the LDS scale stage holds 256 columns x (64 + 1) floats. At 32 the
+// 64-row Llama LM head (128256 x 4096) was split in two: 290 against 242 us unsplit.
+constexpr int kDgScaleGroups = 64;
 
 // Largest M served by the single-launch skinny kernel.
 constexpr int kSkinnyMaxM = 32;
