@@ -44,6 +44,24 @@ int sq8_paged_attention(const float* qkv, int q_stride, int rows, int head_num, 
                         int table_stride, int block_size, const float* key_cache,
                         const float* value_cache, float* out, void* hip_stream);
 
+/* sq8_paged_attention with a device workspace that lets long rows split their positions over
+ * several workgroups: the flash-decoding split and its combine kernel
+ * (src/source/op/kernels/cuda/paged_kernels.cu:96-294), here one launch whose last-finishing
+ * chunk per (row, kv head) merges the chunks. The workspace must be zero-filled
+ * before its first use (every call leaves it ready for the next); calls that share a workspace
+ * must not overlap. workspace == NULL, or a shape for which
+ * sq8_paged_attention_workspace_bytes() is 0, runs the unsplit kernel. */
+int sq8_paged_attention_ws(const float* qkv, int q_stride, int rows, int head_num,
+                           int kv_head_num, int head_size, const int32_t* positions,
+                           const int32_t* block_table, int table_stride, int block_size,
+                           const float* key_cache, const float* value_cache, float* out,
+                           void* workspace, size_t workspace_bytes, void* hip_stream);
+
+/* Workspace bytes sq8_paged_attention_ws uses for any call of at most `rows` rows of this shape
+ * (0: it never splits). */
+size_t sq8_paged_attention_workspace_bytes(int rows, int head_num, int kv_head_num,
+                                           int head_size, int table_stride, int block_size);
+
 /* out[r][i] = silu(gate_up[r][i]) * gate_up[r][ffn + i] for the fused gate/up projection rows
  * [w1 x | w3 x] (swiglu_kernel_cu_fp32, src/source/op/kernels/cuda/swiglu_kernel.cu:4-21, on the
  * separate w1 and w3 outputs). */

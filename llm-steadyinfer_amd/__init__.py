@@ -34,7 +34,8 @@ DECODE_SYMBOLS = ("sq8_embedding", "sq8_rmsnorm", "sq8_add_rmsnorm", "sq8_rope_t
                   "sq8_argmax", "sq8_quantize", "sq8_step_advance", "sq8_matmul_rmsnorm",
                   "sq8_matmul_swiglu", "sq8_rope_attention_decode")
 # include/sq8_batch.h
-BATCH_SYMBOLS = ("sq8_paged_rope_kv", "sq8_paged_attention", "sq8_swiglu_rows", "sq8_argmax_rows")
+BATCH_SYMBOLS = ("sq8_paged_rope_kv", "sq8_paged_attention", "sq8_paged_attention_ws",
+                 "sq8_paged_attention_workspace_bytes", "sq8_swiglu_rows", "sq8_argmax_rows")
 
 _lib = None
 
@@ -86,6 +87,7 @@ def lib() -> ctypes.CDLL:
             "sq8_rope_attention_decode": [vp, I, I, I, vp, vp, vp, vp, vp, vp, I, vp],
             "sq8_paged_rope_kv": [vp, I, I, I, I, vp, vp, I, I, vp, vp, vp, vp, vp],
             "sq8_paged_attention": [vp, I, I, I, I, I, vp, vp, I, I, vp, vp, vp, vp],
+            "sq8_paged_attention_ws": [vp, I, I, I, I, I, vp, vp, I, I, vp, vp, vp, vp, sz, vp],
             "sq8_swiglu_rows": [vp, I, I, vp, vp],
             "sq8_argmax_rows": [vp, I, I, vp, vp],
         }
@@ -95,6 +97,8 @@ def lib() -> ctypes.CDLL:
             fn.restype = I
         L.sq8_argmax_workspace_bytes.argtypes = [I]
         L.sq8_argmax_workspace_bytes.restype = sz
+        L.sq8_paged_attention_workspace_bytes.argtypes = [I, I, I, I, I, I]
+        L.sq8_paged_attention_workspace_bytes.restype = sz
         _lib = L
     return _lib
 
@@ -311,13 +315,29 @@ def paged_rope_kv(qkv, head_num: int, kv_head_num: int, head_size: int, position
           _ptr(kcache), _ptr(vcache), stream=stream)
 
 
+def paged_attention_workspace_bytes(rows: int, head_num: int, kv_head_num: int, head_size: int,
+                                    table_stride: int, block_size: int) -> int:
+    """Bytes of the split-KV workspace for this shape (0: the kernel never splits it)."""
+    return int(lib().sq8_paged_attention_workspace_bytes(rows, head_num, kv_head_num, head_size,
+                                                         table_stride, block_size))
+
+
 def paged_attention(qkv, q_stride: int, head_num: int, kv_head_num: int, head_size: int,
-                    positions, block_table, block_size: int, kcache, vcache, out, stream=None):
-    """out[r] = attention of row r's query heads over positions 0..positions[r] of its sequence."""
+                    positions, block_table, block_size: int, kcache, vcache, out, workspace=None,
+                    stream=None):
+    """out[r] = attention of row r's query heads over positions 0..positions[r] of its sequence.
+    With a workspace (zero-filled before its first use, of at least
+    paged_attention_workspace_bytes() bytes) long rows split over several workgroups."""
     rows = positions.numel()
-    _call("sq8_paged_attention", _ptr(qkv), q_stride, rows, head_num, kv_head_num, head_size,
-          _ptr(positions), _ptr(block_table), block_table.shape[-1], block_size, _ptr(kcache),
-          _ptr(vcache), _ptr(out), stream=stream)
+    if workspace is None:
+        _call("sq8_paged_attention", _ptr(qkv), q_stride, rows, head_num, kv_head_num, head_size,
+              _ptr(positions), _ptr(block_table), block_table.shape[-1], block_size,
+              _ptr(kcache), _ptr(vcache), _ptr(out), stream=stream)
+    else:
+        _call("sq8_paged_attention_ws", _ptr(qkv), q_stride, rows, head_num, kv_head_num,
+              head_size, _ptr(positions), _ptr(block_table), block_table.shape[-1], block_size,
+              _ptr(kcache), _ptr(vcache), _ptr(out), _ptr(workspace),
+              workspace.numel() * workspace.element_size(), stream=stream)
 
 
 def swiglu_rows(gate_up, out, stream=None):

@@ -34,14 +34,16 @@ import numpy as np
 
 from . import (SQ8_EPI_NONE, SQ8_EPI_RESIDUAL, SQ8_EPI_SWIGLU, Workspace, add_rmsnorm,
                argmax_rows, embedding, epilogue_fused, lib, matmul, matmul_epilogue,
-               paged_attention, paged_rope_kv, rmsnorm, rope_tables, swiglu_rows)
+               paged_attention, paged_attention_workspace_bytes, paged_rope_kv, rmsnorm,
+               rope_tables, swiglu_rows)
 
 EPS = 1e-6
 
 
 class PagedBatchModel:
     def __init__(self, cfg, weights: dict, group_size: int, max_rows: int, max_seq_len: int,
-                 num_blocks: int, block_size: int, device="cuda", use_graphs: bool = True):
+                 num_blocks: int, block_size: int, device="cuda", use_graphs: bool = True,
+                 split_kv: bool = True):
         import torch
         self.torch = torch
         self.cfg, self.w, self.gs = cfg, weights, group_size
@@ -83,13 +85,19 @@ class PagedBatchModel:
                     need = max(need, int(lib().sq8_epilogue_workspace_bytes(B, N, K, group_size,
                                                                             epi)))
         self.ws.get(need)
+        # Split-KV attention workspace (zero-filled once; each call leaves its tickets zero).
+        att_need = paged_attention_workspace_bytes(R, cfg.head_num, cfg.kv_head_num, self.hs,
+                                                   self.max_blocks_per_seq, block_size)
+        self.att_ws = (torch.zeros((att_need + 3) // 4, **i32) if split_kv and att_need > 0
+                       else None)
 
     @classmethod
     def from_decoder(cls, dec, max_rows: int, max_seq_len: int, num_blocks: int,
-                     block_size: int, use_graphs: bool = True) -> "PagedBatchModel":
+                     block_size: int, use_graphs: bool = True,
+                     split_kv: bool = True) -> "PagedBatchModel":
         """Share the fused weights of an Int8Decoder (model file or random init)."""
         return cls(dec.cfg, dec.w, dec.gs, max_rows, max_seq_len, num_blocks, block_size,
-                   dec.device, use_graphs=use_graphs)
+                   dec.device, use_graphs=use_graphs, split_kv=split_kv)
 
     def kv_bytes_per_position(self) -> int:
         return 2 * 4 * self.cfg.layer_num * self.cfg.kv_dim
@@ -195,7 +203,8 @@ class PagedBatchModel:
                           self.block_size, self.sin, self.cos, self.kcache[l], self.vcache[l],
                           stream=stream)
             paged_attention(qkv, d + 2 * kv, cfg.head_num, cfg.kv_head_num, self.hs, pos, table,
-                            self.block_size, self.kcache[l], self.vcache[l], att, stream=stream)
+                            self.block_size, self.kcache[l], self.vcache[l], att,
+                            workspace=self.att_ws, stream=stream)
             if fuse_o:
                 self._mm_epi(att, w["o"][l], x, SQ8_EPI_RESIDUAL, stream, residual=x)
                 rmsnorm(x, w["norm"][L + l], xn, EPS, stream=stream)

@@ -1,6 +1,7 @@
 // Continuous-batching operators (paged KV cache) for gfx950: rows of different sequences, each at
 // its own position, in one launch. C ABI in include/sq8_batch.h.
 #include <float.h>
+#include <algorithm>
 #include <limits.h>
 #include <math.h>
 
@@ -22,6 +23,24 @@ constexpr int kAttnWaves = SQ8_ATTN_WAVES;  // waves per (row, head) attention w
 constexpr int kAttnChunk = SQ8_ATTN_CHUNK;  // cache positions per wave per load step
 constexpr int kRowU = 2;                   // positions per 16-lane group per step
 constexpr int kAttnTableCap = 4096;        // block-table entries staged in LDS by the row kernel
+// Split-KV attention (sq8_paged_attention_ws): the work-item target per kv head is
+// kAttnFillItems / kv_head_num items when the unsplit grid (rows x kv heads) is below
+// kAttnFillUnits workgroups, else rows / kAttnBalanceDiv (chunks of about kAttnBalanceDiv mean
+// row lengths: only rows longer than that split); chunks are at least kAttnMinChunk positions.
+#ifndef SQ8_ATTN_MIN_CHUNK
+#define SQ8_ATTN_MIN_CHUNK 128
+#endif
+#ifndef SQ8_ATTN_FILL
+#define SQ8_ATTN_FILL 768
+#endif
+#ifndef SQ8_ATTN_BAL
+#define SQ8_ATTN_BAL 1
+#endif
+constexpr int kAttnMinChunk = SQ8_ATTN_MIN_CHUNK;
+constexpr int kAttnFillItems = SQ8_ATTN_FILL;  // 3 four-wave workgroups per CU on 256 CUs
+constexpr int kAttnFillUnits = 512;
+constexpr int kAttnBalanceDiv = SQ8_ATTN_BAL;
+constexpr int kAttnSplitMaxRows = 4096;
 
 hipStream_t stream_of(void* s) { return static_cast<hipStream_t>(s); }
 int launched() { return hipGetLastError() == hipSuccess ? SQ8_OK : SQ8_ERR_LAUNCH; }
@@ -225,12 +244,22 @@ __device__ __forceinline__ float row16_sum(float v) {
 // adds and one exponential and a step needs no cross-group exchange (a wave-wide max per step,
 // through two lane permutes per head, made every step wait on the permute latency). Groups are
 // brought to a common max and summed at the end, then the waves are combined.
+//
+// With n_target > 0 (split KV, the flash-decoding split of paged_kernels.cu:96-294) the rows'
+// positions are cut into chunks of C = max(kAttnMinChunk, ceil(T / n_target)) positions, T the
+// total over all rows, so a row of n positions makes ceil(n / C) work items and there are at most
+// n_target + rows of them per kv head; blockIdx.x / kv_head_num picks a work item (items numbered
+// row by row) and a workgroup past the last item exits at once. A row of one chunk writes its
+// output directly. Otherwise each chunk stores its un-normalised head outputs, max and sum to
+// part (agent-scope stores, acknowledged before the ticket), takes a ticket per (row, kv head),
+// and the chunk that finishes last merges the row's chunks and resets the ticket to zero.
 template <int DPL, int GMAX, int W>
 __global__ __launch_bounds__(W * kWave) void paged_attention_rows_kernel(
     const float* __restrict__ qkv, int q_stride, int head_num, int kv_head_num, int head_size,
     const int32_t* __restrict__ positions, const int32_t* __restrict__ block_table,
     int table_stride, int block_size, const float* kcache, const float* vcache,
-    float* __restrict__ out) {
+    float* __restrict__ out, int rows, int n_target, float* __restrict__ part,
+    unsigned* __restrict__ tickets) {
   constexpr int U = kRowU;
   constexpr int SP = 4 * U;  // positions per wave per step
   constexpr int HS = 16 * DPL;
@@ -238,15 +267,62 @@ __global__ __launch_bounds__(W * kWave) void paged_attention_rows_kernel(
   __shared__ float s_m[W][GMAX], s_l[W][GMAX];
   __shared__ float s_acc[W][GMAX][HS];
   __shared__ int32_t table[kAttnTableCap];  // the row's block table (table_stride <= cap)
+  __shared__ int s_item[3];                 // split KV: row, its first item, chunk length
   const int G = head_num / kv_head_num;
-  const int r = blockIdx.x / kv_head_num, kvh = blockIdx.x % kv_head_num;
-  const int seq = positions[r] + 1;
+  const int item = blockIdx.x / kv_head_num, kvh = blockIdx.x % kv_head_num;
+  int r = item, first = item, chunk = 0;
+  if (n_target > 0) {
+    if (threadIdx.x < kWave) {  // wave 0 finds the work item's row and chunk
+      const int ln = threadIdx.x;
+      int t = 0;
+      for (int i = ln; i < rows; i += kWave) t += positions[i] + 1;
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) t += __shfl_xor(t, d, kWave);
+      const int c = max(kAttnMinChunk, (t + n_target - 1) / n_target);
+      int base = 0, sel = -1, sel_first = 0;
+      for (int i0 = 0; i0 < rows; i0 += kWave) {
+        const int i = i0 + ln;
+        const int n = i < rows ? (positions[i] + c) / c : 0;  // ceil(row length / c)
+        int incl = n;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+          const int v = __shfl_up(incl, d, kWave);
+          if (ln >= d) incl += v;
+        }
+        const int excl = base + incl - n;
+        const uint64_t hit = __ballot(n > 0 && item >= excl && item < base + incl);
+        if (hit) {
+          const int src = __builtin_ctzll(hit);
+          sel = __shfl(i, src, kWave);
+          sel_first = __shfl(excl, src, kWave);
+          break;
+        }
+        base += __shfl(incl, kWave - 1, kWave);
+      }
+      if (ln == 0) {
+        s_item[0] = sel;
+        s_item[1] = sel_first;
+        s_item[2] = c;
+      }
+    }
+    __syncthreads();
+    r = s_item[0];
+    first = s_item[1];
+    chunk = s_item[2];
+    if (r < 0) return;  // uniform across the workgroup
+  }
+  const int row_len = positions[r] + 1;
+  const int p0 = chunk > 0 ? (item - first) * chunk : 0;
+  const int nchunks = chunk > 0 ? (row_len + chunk - 1) / chunk : 1;
+  // Positions below are relative to the first table block of the range, b0 * block_size.
+  const int b0 = p0 / block_size, pbase = p0 - b0 * block_size;
+  const int seq = min(row_len, chunk > 0 ? p0 + chunk : row_len) - p0;  // positions in range
   const int kv_dim = kv_head_num * HS, hoff = kvh * HS;
-  // Stage the row's block table once: every cache-row address then costs an LDS read instead of
-  // a dependent global load ahead of each step's key/value loads.
+  // Stage the range's block-table entries once: every cache-row address then costs an LDS read
+  // instead of a dependent global load ahead of each step's key/value loads.
   {
-    const int32_t* gt = block_table + static_cast<size_t>(r) * table_stride;
-    const int nb = (seq + block_size - 1) / block_size;
+    const int32_t* gt = block_table + static_cast<size_t>(r) * table_stride + b0;
+    const int nb = (pbase + seq + block_size - 1) / block_size;
     for (int i = threadIdx.x; i < nb; i += W * kWave) table[i] = gt[i];
     __syncthreads();
   }
@@ -266,7 +342,8 @@ __global__ __launch_bounds__(W * kWave) void paged_attention_rows_kernel(
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const size_t base =
-          paged_row(table, min(posn(c, u), seq - 1), block_size, kv_dim) + hoff + DPL * li;
+          paged_row(table, pbase + min(posn(c, u), seq - 1), block_size, kv_dim) + hoff +
+          DPL * li;
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         kb[b][u][i] = *reinterpret_cast<const float4*>(kcache + base + 4 * i);
@@ -370,6 +447,10 @@ __global__ __launch_bounds__(W * kWave) void paged_attention_rows_kernel(
     }
   }
   __syncthreads();
+  // Partials of (row, kv head) chunk c: G head outputs of HS floats, then G maxima, then G sums.
+  const int pstride = G * (HS + 2);
+  const size_t pitem = static_cast<size_t>(kv_head_num) * pstride;  // floats per work item
+  float* const pbuf = part + (static_cast<size_t>(first) * kv_head_num + kvh) * pstride;
   for (int e = threadIdx.x; e < G * HS; e += W * kWave) {
     const int g = e / HS, d = e % HS;
     float mx = s_m[0][g];
@@ -382,8 +463,69 @@ __global__ __launch_bounds__(W * kWave) void paged_attention_rows_kernel(
       o = fmaf(s_acc[w][g][d], f, o);
       lt = fmaf(s_l[w][g], f, lt);
     }
+    if (nchunks == 1) {
+      out[(static_cast<size_t>(r) * head_num + kvh * G + g) * HS + d] = o / lt;
+    } else {
+      float* const c = pbuf + static_cast<size_t>(item - first) * pitem;
+      __hip_atomic_store(c + e, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (d == 0) {
+        __hip_atomic_store(c + G * HS + g, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(c + G * HS + G + g, lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  if (nchunks == 1) return;
+  // Wait until this thread's partial stores are acknowledged (s_waitcnt with every counter at
+  // zero) before the workgroup takes its ticket.
+  __builtin_amdgcn_s_waitcnt(0);
+  __shared__ bool is_last;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    is_last = __hip_atomic_fetch_add(&tickets[r * kv_head_num + kvh], 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT) ==
+              static_cast<unsigned>(nchunks - 1);
+  __syncthreads();
+  if (!is_last) return;
+  // Merge in batches of kMergeBatch chunks, every load of a batch issued before any is used (one
+  // memory latency per batch, not per chunk), with a running max across batches.
+  constexpr int kMergeBatch = 8;
+  for (int e = threadIdx.x; e < G * HS; e += W * kWave) {
+    const int g = e / HS, d = e % HS;
+    float mx = -INFINITY, o = 0.f, lt = 0.f;
+    for (int c0 = 0; c0 < nchunks; c0 += kMergeBatch) {
+      float mv[kMergeBatch], lv[kMergeBatch], ov[kMergeBatch];
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) {
+        const float* const pc = pbuf + static_cast<size_t>(min(c0 + k, nchunks - 1)) * pitem;
+        mv[k] = __hip_atomic_load(pc + G * HS + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        lv[k] = __hip_atomic_load(pc + G * HS + G + g, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+        ov[k] = __hip_atomic_load(pc + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      // Chunks past the row's last repeat the last chunk and are skipped; every chunk has at
+      // least one position, so its max is finite.
+      float bm = mx;
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k)
+        if (c0 + k < nchunks) bm = fmaxf(bm, mv[k]);
+      const float f0 = mx == -INFINITY ? 0.f : expf(mx - bm);
+      o *= f0;
+      lt *= f0;
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) {
+        if (c0 + k < nchunks) {
+          const float f = expf(mv[k] - bm);
+          o = fmaf(ov[k], f, o);
+          lt = fmaf(lv[k], f, lt);
+        }
+      }
+      mx = bm;
+    }
     out[(static_cast<size_t>(r) * head_num + kvh * G + g) * HS + d] = o / lt;
   }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(&tickets[r * kv_head_num + kvh], 0u, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ __launch_bounds__(kBlock) void swiglu_rows_kernel(const float* __restrict__ gu,
@@ -455,6 +597,22 @@ __global__ __launch_bounds__(kArgBlock) void argmax_rows_kernel(const float* __r
   }
 }
 
+// Shapes the (row, kv head) kernel covers.
+bool rows_kernel_fits(int head_size, int G) {
+  return (head_size == 128 || head_size == 64) && G <= 8;
+}
+// Work-item target per kv head of split-KV attention (0: no split).
+int split_target(int rows, int kv_head_num, int table_stride, int block_size) {
+  if (rows > kAttnSplitMaxRows || table_stride >= kAttnTableCap ||
+      static_cast<int64_t>(table_stride) * block_size <= kAttnMinChunk)
+    return 0;
+  const int64_t units = static_cast<int64_t>(rows) * kv_head_num;
+  const int fill = units < kAttnFillUnits ? (kAttnFillItems + kv_head_num - 1) / kv_head_num : 0;
+  return max(max(fill, rows / kAttnBalanceDiv), 1);
+}
+// Ticket area at the start of the split-KV workspace (one per (row, kv head), 256-byte aligned).
+int64_t ticket_bytes(int64_t units) { return (units * 4 + 255) / 256 * 256; }
+
 }  // namespace
 }  // namespace sq8
 
@@ -482,6 +640,33 @@ int sq8_paged_attention(const float* qkv, int q_stride, int rows, int head_num, 
                         int head_size, const int32_t* positions, const int32_t* block_table,
                         int table_stride, int block_size, const float* key_cache,
                         const float* value_cache, float* out, void* hip_stream) {
+  return sq8_paged_attention_ws(qkv, q_stride, rows, head_num, kv_head_num, head_size, positions,
+                                block_table, table_stride, block_size, key_cache, value_cache,
+                                out, nullptr, 0, hip_stream);
+}
+
+size_t sq8_paged_attention_workspace_bytes(int rows, int head_num, int kv_head_num,
+                                           int head_size, int table_stride, int block_size) {
+  if (rows <= 0 || head_num <= 0 || kv_head_num <= 0 || head_num % kv_head_num ||
+      table_stride <= 0 || block_size <= 0)
+    return 0;
+  const int G = head_num / kv_head_num;
+  if (!rows_kernel_fits(head_size, G)) return 0;
+  if (split_target(rows, kv_head_num, table_stride, block_size) == 0) return 0;
+  // Enough for every call of at most `rows` rows (the item count is not monotone in rows: small
+  // batches fill the GPU with more items).
+  int64_t items = 0;
+  for (int n = 1; n <= rows; ++n)
+    items = std::max<int64_t>(items, split_target(n, kv_head_num, table_stride, block_size) + n);
+  const int64_t units = static_cast<int64_t>(rows) * kv_head_num;
+  return static_cast<size_t>(ticket_bytes(units) + items * kv_head_num * G * (head_size + 2) * 4);
+}
+
+int sq8_paged_attention_ws(const float* qkv, int q_stride, int rows, int head_num,
+                           int kv_head_num, int head_size, const int32_t* positions,
+                           const int32_t* block_table, int table_stride, int block_size,
+                           const float* key_cache, const float* value_cache, float* out,
+                           void* workspace, size_t workspace_bytes, void* hip_stream) {
   if (!qkv || !positions || !block_table || !key_cache || !value_cache || !out)
     return SQ8_ERR_NULL;
   if (rows <= 0 || head_num <= 0 || kv_head_num <= 0 || head_num % kv_head_num ||
@@ -492,15 +677,26 @@ int sq8_paged_attention(const float* qkv, int q_stride, int rows, int head_num, 
   const int G = head_num / kv_head_num;
   const bool k16 = reinterpret_cast<uintptr_t>(key_cache) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(value_cache) % 16 == 0;
-  if ((head_size == 128 || head_size == 64) && G <= 8 && k16 && table_stride <= kAttnTableCap &&
-      static_cast<int64_t>(rows) * kv_head_num <= 0x7fffffff) {
-    // Few workgroups (few, typically long, rows): 8 waves each to keep more rows in flight.
-    const bool wide = static_cast<int64_t>(rows) * kv_head_num < 2 * cu_count();
-    const dim3 grid(rows * kv_head_num), block((wide ? 8 : 4) * kWave);
+  const size_t need = sq8_paged_attention_workspace_bytes(rows, head_num, kv_head_num, head_size,
+                                                          table_stride, block_size);
+  if (need > 0 && workspace && workspace_bytes < need) return SQ8_ERR_WORKSPACE;
+  const bool split = need > 0 && workspace != nullptr && k16;
+  if (rows_kernel_fits(head_size, G) && k16 &&
+      (split || table_stride <= kAttnTableCap)) {
+    // Unsplit with few workgroups (few, typically long, rows): 8 waves each to keep more rows
+    // in flight. Split: a workgroup of 4 waves per work item.
+    const int64_t units = static_cast<int64_t>(rows) * kv_head_num;
+    const bool wide = !split && units < 2 * cu_count();
+    const int target = split ? split_target(rows, kv_head_num, table_stride, block_size) : 0;
+    unsigned* tickets = split ? static_cast<unsigned*>(workspace) : nullptr;
+    float* part = split ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                                   ticket_bytes(units))
+                        : nullptr;
+    const dim3 grid((rows + target) * kv_head_num), block((wide ? 8 : 4) * kWave);
     const auto rk = [&](auto kernel) {
       hipLaunchKernelGGL(kernel, grid, block, 0, st, qkv, q_stride, head_num, kv_head_num,
                          head_size, positions, block_table, table_stride, block_size, key_cache,
-                         value_cache, out);
+                         value_cache, out, rows, target, part, tickets);
     };
     if (head_size == 64)
       wide ? rk(paged_attention_rows_kernel<4, 8, 8>) : rk(paged_attention_rows_kernel<4, 8, 4>);

@@ -86,6 +86,61 @@ def test_paged_attention_matches_oracle(sq8, dev, heads, kv_heads, hs, block_siz
         assert err < 2e-6, (i, s, p, err)
 
 
+def test_split_kv_workspace_bytes(sq8):
+    """Split-KV workspace: none when a table row spans at most 128 positions, the row kernel does
+    not cover the head shape or the table row does not fit its LDS; otherwise 256-byte-aligned
+    tickets per (row, kv head) plus G * (head_size + 2) floats per (work item, kv head), with
+    768 / kv_head_num work items (fewer than 512 row-kv-head pairs) or rows, plus rows, at
+    most over every row count up to rows."""
+    f = sq8.paged_attention_workspace_bytes
+    assert f(8, 32, 8, 128, 8, 16) == 0             # 128 positions: never split
+    assert f(8, 32, 8, 256, 64, 16) == 0            # head_size 256: generic kernel
+    assert f(8, 32, 8, 128, 4096, 16) == 0          # table row beyond the LDS stage
+    assert f(8, 32, 8, 128, 16, 16) == 256 + (96 + 8) * 8 * 4 * 130 * 4
+    # 64 rows: 64 + 64 items; 63 rows (504 pairs): 96 + 63, the most for up to 64 rows
+    assert f(64, 32, 8, 128, 68, 16) == 2048 + (96 + 63) * 8 * 4 * 130 * 4
+    assert f(1, 28, 4, 64, 300, 4) == 256 + (192 + 1) * 4 * 7 * 66 * 4
+    assert f(3, 32, 8, 128, 68, 16) < f(4, 32, 8, 128, 68, 16)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads,kv_heads,hs,block_size", [(32, 8, 128, 16), (4, 2, 64, 4),
+                                                          (14, 2, 64, 1), (16, 2, 128, 32)])
+def test_split_kv_attention_matches_oracle(sq8, dev, heads, kv_heads, hs, block_size):
+    """Rows of 1..1500 positions cut into work items of at least 128 positions (chunk length set
+    by the total over the rows) and merged by the last chunk to finish: equal to the oracle to
+    the unsplit kernel's bound. Three calls on one workspace (9 rows, 64 rows at random
+    positions, 3 rows) check that each call leaves its tickets ready for the next."""
+    import torch
+    rng = np.random.default_rng(heads + 7 * hs + block_size)
+    lens = [1, 256, 257, 512, 1500, 700, 3]
+    kv = kv_heads * hs
+    kc, vc, tables, K, V = _paged_case(rng, lens, kv, block_size, extra_blocks=3)
+    dim = heads * hs
+    stride = dim + 2 * kv
+    tab_all = np.array(tables, np.int32)
+    many = [(s, int(rng.integers(0, lens[s]))) for s in rng.integers(0, len(lens), 64)]
+    ws = torch.zeros((sq8.paged_attention_workspace_bytes(
+        64, heads, kv_heads, hs, tab_all.shape[1], block_size) + 3) // 4,
+        dtype=torch.int32, device=dev)
+    assert ws.numel() > 0
+    kc_t, vc_t = _t(kc, dev), _t(vc, dev)
+    for rows in ([(s, n - 1) for s, n in enumerate(lens)] + [(4, 255), (4, 256)],
+                 many, [(1, 255), (4, 1000), (5, 10)]):
+        qkv = rng.standard_normal((len(rows), stride)).astype(np.float32)
+        pos = np.array([p for _, p in rows], np.int32)
+        tab = np.array([tables[s] for s, _ in rows], np.int32)
+        out = torch.full((len(rows), dim), float("nan"), device=dev)
+        sq8.paged_attention(_t(qkv, dev), stride, heads, kv_heads, hs, _t(pos, dev),
+                            _t(tab, dev), block_size, kc_t, vc_t, out, workspace=ws)
+        got = out.cpu().numpy()
+        for i, (s, p) in enumerate(rows):
+            ref = do.attention(qkv[i, :dim], K[s], V[s], p, heads, kv_heads, hs)
+            err = np.max(np.abs(got[i] - ref)) / max(np.max(np.abs(ref)), 1e-30)
+            assert err < 2e-6, (rows, i, s, p, err)
+        assert int(ws[:tab.shape[0] * kv_heads].abs().sum()) == 0  # tickets back at zero
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("heads,kv_heads,hs,block_size", [(4, 2, 64, 4), (12, 2, 128, 16)])
 def test_paged_rope_kv_writes_slots(sq8, dev, heads, kv_heads, hs, block_size):
@@ -184,3 +239,33 @@ def test_continuous_batching_matches_oracle(dev, tmp_path, max_batch, block_size
     if max_batch > 64:  # the 88 prompt tokens start as one step: the fused-epilogue GEMM path
         assert model.fused(88) == (True, True, True)
     assert got == ref
+
+
+@pytest.mark.gpu
+def test_continuous_batching_long_rows_split_kv(dev, tmp_path):
+    """Prompts of up to 300 tokens with a 320-position table row: attention rows past 256
+    positions take the split-KV path (the model's workspace is allocated), in graph-replayed
+    decode steps and eager prefill steps alike; every sequence's greedy tokens equal the float64
+    oracle decoding it alone."""
+    sched = importlib.import_module("llm_steadyinfer_amd.scheduler")
+    bm = importlib.import_module("llm_steadyinfer_amd.batch_model")
+    dec = importlib.import_module("llm_steadyinfer_amd.decoder")
+    cfg = mf.ModelConfig(dim=256, hidden_dim=512, layer_num=2, head_num=4, kv_head_num=2,
+                         vocab_size=-1000, seq_len=320, rope_theta=1e6)
+    path = mf.write_random(tmp_path / "m.bin", cfg, 64, seed=12, w_std=0.2)
+    rng = np.random.default_rng(12)
+    prompts = [rng.integers(0, cfg.vocab, n).tolist() for n in (270, 5, 300, 256)]
+    n_new, max_seq = 10, 320
+    ref = [do.DecodeModel(mf.ModelFile(path), max_seq=max_seq).generate(p, n_new)[0]
+           for p in prompts]
+    D = dec.Int8Decoder.from_file(path, max_seq=max_seq, device=dev)
+    s = sched.Scheduler(None, max_batch=4, max_seq_len=max_seq, max_gen_len=n_new, block_size=4)
+    model = bm.PagedBatchModel.from_decoder(D, max_rows=4, max_seq_len=max_seq,
+                                            num_blocks=s.alloc.num_blocks, block_size=4)
+    assert model.att_ws is not None
+    s.forward = model.forward
+    for p in prompts:
+        assert s.add_request(p) >= 0
+    done = s.run(max_steps=5000)
+    assert model.graph_replays > 0
+    assert [q.generated_tokens for q in done] == ref
