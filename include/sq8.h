@@ -78,6 +78,20 @@ int sq8_matmul_epilogue(const float* x, const int8_t* w, const float* scales, fl
 /* Workspace bytes of sq8_matmul_epilogue (includes the product buffer of unfused paths). */
 size_t sq8_epilogue_workspace_bytes(int M, int N, int K, int group_size, int epilogue);
 
+/* y = epilogue(rmsnorm(x + res) * norm_w . W^T) for M token rows: the reference's residual add
+ * and RMSNorm ahead of the QKV and gate/up projections (llama3.cpp:1021-1045, 1139-1150;
+ * add_kernel.cu, rmsnorm_kernel.cu:8-160), with x + res written back to x (res may be NULL:
+ * x is only read). epilogue is SQ8_EPI_NONE or SQ8_EPI_SWIGLU (y is then [M][N/2]). Where
+ * sq8_rmsnorm_rows_fused() is 1 (the MFMA tile and decode-GEMM paths, K <= 16384) the norm is
+ * formed while the activation rows are converted for the MFMAs, in the same launch; elsewhere
+ * it runs as sq8_add_rmsnorm / sq8_rmsnorm into the workspace, then sq8_matmul_epilogue. */
+int sq8_matmul_rmsnorm_rows(float* x, const float* res, const float* norm_w, float eps,
+                            const int8_t* w, const float* scales, float* y, int M, int N, int K,
+                            int group_size, int epilogue, void* workspace,
+                            size_t workspace_bytes, void* hip_stream);
+int sq8_rmsnorm_rows_fused(int M, int N, int K, int group_size, int epilogue);
+size_t sq8_rmsnorm_rows_workspace_bytes(int M, int N, int K, int group_size, int epilogue);
+
 /* 1 if sq8_matmul_epilogue fuses the epilogue into the matmul kernel for this shape, else 0. */
 int sq8_epilogue_fused(int M, int N, int K, int group_size);
 

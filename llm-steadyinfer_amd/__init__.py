@@ -22,7 +22,9 @@ SQ8_ERR_LAUNCH = -5
 SQ8_ERR_DEVICE = -6
 
 EXPORTED_SYMBOLS = ("sq8_matmul", "sq8_workspace_bytes", "sq8_status_string", "sq8_path_name",
-                    "sq8_matmul_epilogue", "sq8_epilogue_workspace_bytes", "sq8_epilogue_fused")
+                    "sq8_matmul_epilogue", "sq8_epilogue_workspace_bytes", "sq8_epilogue_fused",
+                    "sq8_matmul_rmsnorm_rows", "sq8_rmsnorm_rows_fused",
+                    "sq8_rmsnorm_rows_workspace_bytes")
 
 # Output epilogues (include/sq8.h, enum sq8_epilogue).
 SQ8_EPI_NONE = 0
@@ -67,6 +69,13 @@ def lib() -> ctypes.CDLL:
         L.sq8_matmul_epilogue.restype = I
         L.sq8_epilogue_workspace_bytes.argtypes = [I, I, I, I, I]
         L.sq8_epilogue_workspace_bytes.restype = sz
+        L.sq8_matmul_rmsnorm_rows.argtypes = [vp, vp, vp, ctypes.c_float, vp, vp, vp, I, I, I,
+                                               I, I, vp, sz, vp]
+        L.sq8_matmul_rmsnorm_rows.restype = I
+        L.sq8_rmsnorm_rows_fused.argtypes = [I, I, I, I, I]
+        L.sq8_rmsnorm_rows_fused.restype = I
+        L.sq8_rmsnorm_rows_workspace_bytes.argtypes = [I, I, I, I, I]
+        L.sq8_rmsnorm_rows_workspace_bytes.restype = sz
         L.sq8_epilogue_fused.argtypes = [I, I, I, I]
         L.sq8_epilogue_fused.restype = I
         f32 = ctypes.c_float
@@ -193,6 +202,37 @@ def matmul_epilogue(x, w, scales, y, epilogue: int, residual=None, group_size: i
     rc = int(lib().sq8_matmul_epilogue(x.data_ptr(), w.data_ptr(), scales.data_ptr(),
                                        y.data_ptr(), M, N, K, group_size, epilogue,
                                        _ptr(residual), ws_ptr or None, ws_n, stream.cuda_stream))
+    if rc != SQ8_OK:
+        raise Sq8Error(rc)
+    return y
+
+
+def rmsnorm_rows_fused(M: int, N: int, K: int, group_size: int = 64,
+                       epilogue: int = SQ8_EPI_NONE) -> bool:
+    """Whether sq8_matmul_rmsnorm_rows forms the norm inside the matmul's launches here."""
+    return bool(lib().sq8_rmsnorm_rows_fused(M, N, K, group_size, epilogue))
+
+
+def matmul_rmsnorm_rows(x, res, norm_w, eps: float, w, scales, y, epilogue: int = SQ8_EPI_NONE,
+                        group_size: int = 64, workspace: Workspace | None = None, stream=None):
+    """y = epilogue(rmsnorm(x + res) * norm_w @ dequant(w, scales).T); x + res is written back
+    to x (res may be None: x is only read)."""
+    import torch
+    M, K = x.shape
+    N = w.shape[0]
+    for t in (x, w, scales, y, norm_w) + ((res,) if res is not None else ()):
+        if not t.is_contiguous():
+            raise ValueError("sq8 tensors must be contiguous")
+    if stream is None:
+        stream = torch.cuda.current_stream(x.device)
+    if workspace is None:
+        workspace = _default_ws.setdefault(str(x.device), Workspace(x.device))
+    ws_ptr, ws_n = workspace.get(int(lib().sq8_rmsnorm_rows_workspace_bytes(M, N, K, group_size,
+                                                                             epilogue)))
+    rc = int(lib().sq8_matmul_rmsnorm_rows(x.data_ptr(), _ptr(res), norm_w.data_ptr(), eps,
+                                           w.data_ptr(), scales.data_ptr(), y.data_ptr(), M, N,
+                                           K, group_size, epilogue, ws_ptr or None, ws_n,
+                                           stream.cuda_stream))
     if rc != SQ8_OK:
         raise Sq8Error(rc)
     return y

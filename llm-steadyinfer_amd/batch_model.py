@@ -34,6 +34,7 @@ import numpy as np
 
 from . import (SQ8_EPI_NONE, SQ8_EPI_RESIDUAL, SQ8_EPI_SWIGLU, Workspace, add_rmsnorm,
                argmax_rows, embedding, epilogue_fused, lib, matmul, matmul_epilogue,
+               matmul_rmsnorm_rows,
                paged_attention, paged_attention_workspace_bytes, paged_rope_kv, rmsnorm,
                rope_tables, swiglu_rows)
 
@@ -43,7 +44,7 @@ EPS = 1e-6
 class PagedBatchModel:
     def __init__(self, cfg, weights: dict, group_size: int, max_rows: int, max_seq_len: int,
                  num_blocks: int, block_size: int, device="cuda", use_graphs: bool = True,
-                 split_kv: bool = True):
+                 split_kv: bool = True, fuse_norm: bool = True):
         import torch
         self.torch = torch
         self.cfg, self.w, self.gs = cfg, weights, group_size
@@ -75,6 +76,7 @@ class PagedBatchModel:
         self.rows_run = 0
         self._fuse = {}
         self.use_graphs = use_graphs
+        self.fuse_norm = fuse_norm
         self.graphs = {}
         self.graph_replays = 0
         # Workspace for every row count and projection, allocated once (graphs keep its address).
@@ -84,6 +86,9 @@ class PagedBatchModel:
                 for epi in (SQ8_EPI_NONE, SQ8_EPI_RESIDUAL, SQ8_EPI_SWIGLU):
                     need = max(need, int(lib().sq8_epilogue_workspace_bytes(B, N, K, group_size,
                                                                             epi)))
+                    if epi != SQ8_EPI_RESIDUAL:
+                        need = max(need, int(lib().sq8_rmsnorm_rows_workspace_bytes(
+                            B, N, K, group_size, epi)))
         self.ws.get(need)
         # Split-KV attention workspace (zero-filled once; each call leaves its tickets zero).
         att_need = paged_attention_workspace_bytes(R, cfg.head_num, cfg.kv_head_num, self.hs,
@@ -93,11 +98,11 @@ class PagedBatchModel:
 
     @classmethod
     def from_decoder(cls, dec, max_rows: int, max_seq_len: int, num_blocks: int,
-                     block_size: int, use_graphs: bool = True,
-                     split_kv: bool = True) -> "PagedBatchModel":
+                     block_size: int, use_graphs: bool = True, split_kv: bool = True,
+                     fuse_norm: bool = True) -> "PagedBatchModel":
         """Share the fused weights of an Int8Decoder (model file or random init)."""
         return cls(dec.cfg, dec.w, dec.gs, max_rows, max_seq_len, num_blocks, block_size,
-                   dec.device, use_graphs=use_graphs, split_kv=split_kv)
+                   dec.device, use_graphs=use_graphs, split_kv=split_kv, fuse_norm=fuse_norm)
 
     def kv_bytes_per_position(self) -> int:
         return 2 * 4 * self.cfg.layer_num * self.cfg.kv_dim
@@ -110,6 +115,23 @@ class PagedBatchModel:
         q, s = qs
         matmul_epilogue(x, q, s, y, epilogue, residual=residual, group_size=self.gs,
                         workspace=self.ws, stream=stream)
+
+    def _mm_norm(self, x, res, norm_w, qs, y, epilogue, xn, stream):
+        """y = epilogue(rmsnorm(x + res) * norm_w . W^T), x += res. With fuse_norm the norm is
+        formed inside the matmul's launches (sq8_matmul_rmsnorm_rows); otherwise through xn."""
+        q, s = qs
+        if self.fuse_norm:
+            matmul_rmsnorm_rows(x, res, norm_w, EPS, q, s, y, epilogue, group_size=self.gs,
+                                workspace=self.ws, stream=stream)
+            return
+        if res is not None:
+            add_rmsnorm(x, res, norm_w, xn, EPS, stream=stream)
+        else:
+            rmsnorm(x, norm_w, xn, EPS, stream=stream)
+        if epilogue == SQ8_EPI_NONE:
+            self._mm(xn, qs, y, stream)
+        else:
+            self._mm_epi(xn, qs, y, epilogue, stream)
 
     def fused(self, B: int):
         """(O, gate/up, down) epilogues fused at B rows."""
@@ -194,11 +216,9 @@ class PagedBatchModel:
         embedding(w["emb"], self.tok[:B], x, stream=stream)
         pending = False  # proj holds the FFN output still to be added to x
         for l in range(L):
-            if pending:  # residual of the previous FFN, then this layer's attention norm
-                add_rmsnorm(x, proj, w["norm"][l], xn, EPS, stream=stream)
-            else:
-                rmsnorm(x, w["norm"][l], xn, EPS, stream=stream)
-            self._mm(xn, w["qkv"][l], qkv, stream)
+            # residual of the previous FFN (if pending), this layer's attention norm, QKV
+            self._mm_norm(x, proj if pending else None, w["norm"][l], w["qkv"][l], qkv,
+                          SQ8_EPI_NONE, xn, stream)
             paged_rope_kv(qkv, cfg.head_num, cfg.kv_head_num, self.hs, pos, table,
                           self.block_size, self.sin, self.cos, self.kcache[l], self.vcache[l],
                           stream=stream)
@@ -207,14 +227,15 @@ class PagedBatchModel:
                             workspace=self.att_ws, stream=stream)
             if fuse_o:
                 self._mm_epi(att, w["o"][l], x, SQ8_EPI_RESIDUAL, stream, residual=x)
-                rmsnorm(x, w["norm"][L + l], xn, EPS, stream=stream)
             else:
                 self._mm(att, w["o"][l], proj, stream)
-                add_rmsnorm(x, proj, w["norm"][L + l], xn, EPS, stream=stream)
+            gres = None if fuse_o else proj  # residual still to be added before the FFN norm
             if fuse_gu:
-                self._mm_epi(xn, w["gu"][l], hid, SQ8_EPI_SWIGLU, stream)
+                self._mm_norm(x, gres, w["norm"][L + l], w["gu"][l], hid, SQ8_EPI_SWIGLU, xn,
+                              stream)
             else:
-                self._mm(xn, w["gu"][l], gu, stream)
+                self._mm_norm(x, gres, w["norm"][L + l], w["gu"][l], gu, SQ8_EPI_NONE, xn,
+                              stream)
                 swiglu_rows(gu, hid, stream=stream)
             if fuse_down:
                 self._mm_epi(hid, w["down"][l], x, SQ8_EPI_RESIDUAL, stream, residual=x)

@@ -119,6 +119,51 @@ int sq8_matmul_epilogue(const float* x, const int8_t* w, const float* scales, fl
   return e == hipSuccess ? SQ8_OK : SQ8_ERR_LAUNCH;
 }
 
+int sq8_rmsnorm_rows_fused(int M, int N, int K, int group_size, int epilogue) {
+  if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0) return 0;
+  if (epilogue != SQ8_EPI_NONE && epilogue != SQ8_EPI_SWIGLU) return 0;
+  if (choose(M, N, K, group_size, true) != Path::kMfma || !sq8::mfma_norm_fused(M, N, K)) return 0;
+  return epilogue == SQ8_EPI_NONE || sq8::mfma_fuses_epilogue(M, N, K);
+}
+
+size_t sq8_rmsnorm_rows_workspace_bytes(int M, int N, int K, int group_size, int epilogue) {
+  if (M <= 0 || N <= 0 || K <= 0 || group_size <= 0) return 0;
+  const size_t base = sq8_epilogue_workspace_bytes(M, N, K, group_size, epilogue);
+  if (sq8_rmsnorm_rows_fused(M, N, K, group_size, epilogue)) return base;
+  // Unfused: the normalised rows follow the matmul's own buffers.
+  return product_offset(base) + static_cast<size_t>(M) * K * sizeof(float);
+}
+
+int sq8_matmul_rmsnorm_rows(float* x, const float* res, const float* norm_w, float eps,
+                            const int8_t* w, const float* scales, float* y, int M, int N, int K,
+                            int group_size, int epilogue, void* workspace,
+                            size_t workspace_bytes, void* hip_stream) {
+  if (!norm_w) return SQ8_ERR_NULL;
+  if (epilogue != SQ8_EPI_NONE && epilogue != SQ8_EPI_SWIGLU) return SQ8_ERR_DIMS;
+  const int v = validate(x, w, scales, y, M, N, K, group_size);
+  if (v != SQ8_OK) return v;
+  if (epilogue == SQ8_EPI_SWIGLU && N % 2 != 0) return SQ8_ERR_DIMS;
+  const size_t need = sq8_rmsnorm_rows_workspace_bytes(M, N, K, group_size, epilogue);
+  if (workspace_bytes < need || (need > 0 && workspace == nullptr)) return SQ8_ERR_WORKSPACE;
+  hipStream_t st = static_cast<hipStream_t>(hip_stream);
+  const bool aligned = aligned16(x) && aligned16(w) && aligned16(norm_w) &&
+                       (!res || aligned16(res));
+  if (aligned && sq8_rmsnorm_rows_fused(M, N, K, group_size, epilogue)) {
+    const sq8::NormArgs na{x, res, norm_w, eps};
+    const hipError_t e = sq8::launch_mfma(x, w, scales, y, M, N, K, group_size, workspace, st,
+                                          sq8::Epi{epilogue, nullptr}, &na);
+    return e == hipSuccess ? SQ8_OK : SQ8_ERR_LAUNCH;
+  }
+  // Unfused: the operators' own RMSNorm into the workspace, then the matmul.
+  const size_t base = sq8_epilogue_workspace_bytes(M, N, K, group_size, epilogue);
+  float* xn = reinterpret_cast<float*>(static_cast<char*>(workspace) + product_offset(base));
+  const int r = res ? sq8_add_rmsnorm(x, res, norm_w, xn, M, K, eps, hip_stream)
+                    : sq8_rmsnorm(x, norm_w, xn, M, K, eps, hip_stream);
+  if (r != SQ8_OK) return r;
+  return sq8_matmul_epilogue(xn, w, scales, y, M, N, K, group_size, epilogue, nullptr, workspace,
+                             base, hip_stream);
+}
+
 const char* sq8_status_string(int status) {
   switch (status) {
     case SQ8_OK: return "ok";

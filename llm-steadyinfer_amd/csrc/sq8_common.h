@@ -52,8 +52,18 @@ int cu_count();
 size_t mfma_workspace_bytes(int M, int N, int K);
 // y = epilogue(x.W^T) (y is [M][N/2] for SwiGLU). Only when mfma_fuses_epilogue(M, N, K); other
 // shapes take launch_mfma with epi.mode == kEpiNone and then launch_epilogue.
+// With na, x is na->x and the activation rows are rmsnorm(x + na->res) * na->w, formed while
+// the rows are packed (x + res is written back to x); only when mfma_norm_fused(M, N, K).
+struct NormArgs {
+  float* x;
+  const float* res;  // may be null
+  const float* w;
+  float eps;
+};
+bool mfma_norm_fused(int M, int N, int K);
 hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
-                       int K, int gs, void* ws, hipStream_t st, Epi epi = Epi{kEpiNone, nullptr});
+                       int K, int gs, void* ws, hipStream_t st, Epi epi = Epi{kEpiNone, nullptr},
+                       const NormArgs* na = nullptr);
 bool mfma_fuses_epilogue(int M, int N, int K);
 hipError_t launch_epilogue(const float* t, float* y, int M, int N, Epi epi, hipStream_t st);
 bool gemv_stream_fits(int M, int K);

@@ -1015,17 +1015,73 @@ __global__ __launch_bounds__(kThreads) void skinny_i8_kernel(
 //    as in the skinny kernels).
 // Per group and column tile: P = sum of the hi and lo MFMAs over both half-steps (from zero),
 // acc += scale[n, g] * P. Result lane l: column l%16, rows 16*rt + 4*(l/16) .. +3.
-__global__ __launch_bounds__(kSplitThreads) void pack_x_kernel(const float* __restrict__ x,
+//
+// With NORM the packed row is rmsnorm(x + res) * nw instead (the reference's add + RMSNorm ahead
+// of a projection, rmsnorm_kernel.cu): x + res is written back to x (res may be null), the row
+// stays in registers (K <= kSplitThreads * 4 * kSplitV) and one workgroup owns the row, so the
+// write-back is in place.
+template <bool NORM>
+__global__ __launch_bounds__(kSplitThreads) void pack_x_kernel(const float* x,
                                                              uint2* __restrict__ xp,
                                                              float* __restrict__ rscale, int M,
-                                                             int K, int RT) {
+                                                             int K, int RT, NormArgs na) {
   __shared__ float red[kSplitThreads / kWave];
   const int m = blockIdx.x;
   const int rt = m >> 4;
   const bool live = m < M;
   const float* xr = x + static_cast<size_t>(min(m, M - 1)) * K;
   float4 v[kSplitV];
-  const int e = load_row_exponent(xr, K, live, v, red);
+  int e;
+  if constexpr (NORM) {
+    const int tid = threadIdx.x;
+    const size_t row = static_cast<size_t>(min(m, M - 1)) * K;
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kSplitV; ++i) {
+      const int k = (tid + i * kSplitThreads) * 4;
+      const bool in = live && k < K;
+      v[i] = in ? *reinterpret_cast<const float4*>(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      if (na.res && in) {
+        const float4 r = *reinterpret_cast<const float4*>(na.res + row + k);
+        v[i] = make_float4(v[i].x + r.x, v[i].y + r.y, v[i].z + r.z, v[i].w + r.w);
+      }
+      ss = fmaf(v[i].x, v[i].x, ss);
+      ss = fmaf(v[i].y, v[i].y, ss);
+      ss = fmaf(v[i].z, v[i].z, ss);
+      ss = fmaf(v[i].w, v[i].w, ss);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off /= 2) ss += __shfl_xor(ss, off, kWave);
+    if ((tid & (kWave - 1)) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float total = red[0];
+#pragma unroll
+    for (int w = 1; w < kSplitThreads / kWave; ++w) total += red[w];
+    const float scale = rsqrtf(total / static_cast<float>(K) + na.eps);
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < kSplitV; ++i) {
+      const int k = (tid + i * kSplitThreads) * 4;
+      if (live && k < K) {
+        if (na.res) *reinterpret_cast<float4*>(na.x + row + k) = v[i];
+        const float4 g = *reinterpret_cast<const float4*>(na.w + k);
+        v[i] = make_float4(scale * v[i].x * g.x, scale * v[i].y * g.y, scale * v[i].z * g.z,
+                           scale * v[i].w * g.w);
+      }
+      amax = fmaxf(amax, absmax4(v[i]));
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off /= 2) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+    __syncthreads();  // every wave has read the sums before red is reused
+    if ((tid & (kWave - 1)) == 0) red[tid >> 6] = amax;
+    __syncthreads();
+    amax = red[0];
+#pragma unroll
+    for (int w = 1; w < kSplitThreads / kWave; ++w) amax = fmaxf(amax, red[w]);
+    e = row_exponent(amax);
+  } else {
+    e = load_row_exponent(xr, K, live, v, red);
+  }
   if (live && threadIdx.x == 0) rscale[m] = ldexpf(1.f, -e);
   for_row_chunks(xr, K, live, v, [&](int k, float4 c) {
     _Float16 h[4], l[4];
@@ -1648,15 +1704,20 @@ hipError_t launch_skinny_i8(const float* x, const int8_t* w, const float* s, flo
 
 template <int RT>
 hipError_t launch_dgemm(const float* x, const int8_t* w, const float* s, float* y, void* ws, int M,
-                        int N, int K, int gs, const Plan& p, hipStream_t st, Epi epi) {
+                        int N, int K, int gs, const Plan& p, hipStream_t st, Epi epi,
+                        const NormArgs* na = nullptr) {
   char* base = static_cast<char*>(ws) + kTicketBytes;
   u32x4* xp = reinterpret_cast<u32x4*>(base);
   base += align256(static_cast<size_t>(K / BK) * RT * 4 * kWave * sizeof(u32x4));
   float* rsc = reinterpret_cast<float*>(base);
   base += align256(static_cast<size_t>(16 * RT) * sizeof(float));
   float* part = reinterpret_cast<float*>(base);
-  hipLaunchKernelGGL(pack_x_kernel, dim3(16 * RT), dim3(kSplitThreads), 0, st, x,
-                     reinterpret_cast<uint2*>(xp), rsc, M, K, RT);
+  if (na)
+    hipLaunchKernelGGL(pack_x_kernel<true>, dim3(16 * RT), dim3(kSplitThreads), 0, st, x,
+                       reinterpret_cast<uint2*>(xp), rsc, M, K, RT, *na);
+  else
+    hipLaunchKernelGGL(pack_x_kernel<false>, dim3(16 * RT), dim3(kSplitThreads), 0, st, x,
+                       reinterpret_cast<uint2*>(xp), rsc, M, K, RT, NormArgs{});
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   auto kern = dgemm_kernel<RT, kDgT, kDgW, dg_depth(RT)>;
@@ -1683,7 +1744,8 @@ hipError_t launch_dgemm(const float* x, const int8_t* w, const float* s, float* 
 
 template <int RT, int T, int W>
 hipError_t launch_tile(const float* x, const int8_t* w, const float* s, float* y, void* ws, int M,
-                       int N, int K, int gs, const Plan& p, hipStream_t st) {
+                       int N, int K, int gs, const Plan& p, hipStream_t st,
+                       const NormArgs* na = nullptr) {
   unsigned* tickets = static_cast<unsigned*>(ws);
   char* base = static_cast<char*>(ws) + kTicketBytes;
   u32x4* xp = reinterpret_cast<u32x4*>(base);
@@ -1691,8 +1753,12 @@ hipError_t launch_tile(const float* x, const int8_t* w, const float* s, float* y
   float* rsc = reinterpret_cast<float*>(base);
   base += align256(static_cast<size_t>(16 * RT) * sizeof(float));
   float* part = reinterpret_cast<float*>(base);
-  hipLaunchKernelGGL(pack_x_kernel, dim3(16 * RT), dim3(kSplitThreads), 0, st, x,
-                     reinterpret_cast<uint2*>(xp), rsc, M, K, RT);
+  if (na)
+    hipLaunchKernelGGL(pack_x_kernel<true>, dim3(16 * RT), dim3(kSplitThreads), 0, st, x,
+                       reinterpret_cast<uint2*>(xp), rsc, M, K, RT, *na);
+  else
+    hipLaunchKernelGGL(pack_x_kernel<false>, dim3(16 * RT), dim3(kSplitThreads), 0, st, x,
+                       reinterpret_cast<uint2*>(xp), rsc, M, K, RT, NormArgs{});
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const dim3 grid((N + 16 * T - 1) / (16 * T), p.splits);
@@ -1733,16 +1799,22 @@ hipError_t launch_epilogue(const float* t, float* y, int M, int N, Epi epi, hipS
   return hipGetLastError();
 }
 
+bool mfma_norm_fused(int M, int N, int K) {
+  const Plan p = make_plan(M, N, K);
+  return (p.tile || p.dgemm) && K % 4 == 0 && K <= kSplitThreads * 4 * kSplitV;
+}
+
 hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
-                       int K, int gs, void* ws, hipStream_t st, Epi epi) {
+                       int K, int gs, void* ws, hipStream_t st, Epi epi, const NormArgs* na) {
   const Plan p = make_plan(M, N, K);
   if (epi.mode != kEpiNone && (p.tile || p.skinny)) return hipErrorInvalidValue;
+  if (na && !mfma_norm_fused(M, N, K)) return hipErrorInvalidValue;
   if (p.dgemm) {
     switch (p.rt) {
-      case 1: return launch_dgemm<1>(x, w, s, y, ws, M, N, K, gs, p, st, epi);
-      case 2: return launch_dgemm<2>(x, w, s, y, ws, M, N, K, gs, p, st, epi);
-      case 3: return launch_dgemm<3>(x, w, s, y, ws, M, N, K, gs, p, st, epi);
-      default: return launch_dgemm<4>(x, w, s, y, ws, M, N, K, gs, p, st, epi);
+      case 1: return launch_dgemm<1>(x, w, s, y, ws, M, N, K, gs, p, st, epi, na);
+      case 2: return launch_dgemm<2>(x, w, s, y, ws, M, N, K, gs, p, st, epi, na);
+      case 3: return launch_dgemm<3>(x, w, s, y, ws, M, N, K, gs, p, st, epi, na);
+      default: return launch_dgemm<4>(x, w, s, y, ws, M, N, K, gs, p, st, epi, na);
     }
   }
   unsigned* tickets = static_cast<unsigned*>(ws);
@@ -1750,14 +1822,14 @@ hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y
   if (p.tile) {
     const int key = p.rt * 100 + p.tn * 10 + (p.tw >= 8 ? 8 : p.tw);
     switch (key) {
-      case 128: return launch_tile<1, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st);
-      case 144: return launch_tile<1, 4, 4>(x, w, s, y, ws, M, N, K, gs, p, st);
-      case 228: return launch_tile<2, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st);
-      case 244: return launch_tile<2, 4, 4>(x, w, s, y, ws, M, N, K, gs, p, st);
-      case 328: return launch_tile<3, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st);
-      case 342: return launch_tile<3, 4, 2>(x, w, s, y, ws, M, N, K, gs, p, st);
-      case 428: return launch_tile<4, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st);
-      case 442: return launch_tile<4, 4, 2>(x, w, s, y, ws, M, N, K, gs, p, st);
+      case 128: return launch_tile<1, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st, na);
+      case 144: return launch_tile<1, 4, 4>(x, w, s, y, ws, M, N, K, gs, p, st, na);
+      case 228: return launch_tile<2, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st, na);
+      case 244: return launch_tile<2, 4, 4>(x, w, s, y, ws, M, N, K, gs, p, st, na);
+      case 328: return launch_tile<3, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st, na);
+      case 342: return launch_tile<3, 4, 2>(x, w, s, y, ws, M, N, K, gs, p, st, na);
+      case 428: return launch_tile<4, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st, na);
+      case 442: return launch_tile<4, 4, 2>(x, w, s, y, ws, M, N, K, gs, p, st, na);
       default: return hipErrorInvalidValue;
     }
   }
