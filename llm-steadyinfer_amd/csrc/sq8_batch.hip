@@ -603,8 +603,10 @@ bool rows_kernel_fits(int head_size, int G) {
 }
 // Work-item target per kv head of split-KV attention (0: no split).
 int split_target(int rows, int kv_head_num, int table_stride, int block_size) {
-  if (rows > kAttnSplitMaxRows || table_stride >= kAttnTableCap ||
-      static_cast<int64_t>(table_stride) * block_size <= kAttnMinChunk)
+  // The kernel sums the rows' lengths (each at most table_stride * block_size) in 32 bits.
+  const int64_t span = static_cast<int64_t>(table_stride) * block_size;
+  if (rows > kAttnSplitMaxRows || table_stride >= kAttnTableCap || span <= kAttnMinChunk ||
+      span * rows > INT_MAX)
     return 0;
   const int64_t units = static_cast<int64_t>(rows) * kv_head_num;
   const int fill = units < kAttnFillUnits ? (kAttnFillItems + kv_head_num - 1) / kv_head_num : 0;
@@ -652,12 +654,14 @@ size_t sq8_paged_attention_workspace_bytes(int rows, int head_num, int kv_head_n
     return 0;
   const int G = head_num / kv_head_num;
   if (!rows_kernel_fits(head_size, G)) return 0;
-  if (split_target(rows, kv_head_num, table_stride, block_size) == 0) return 0;
   // Enough for every call of at most `rows` rows (the item count is not monotone in rows: small
   // batches fill the GPU with more items).
   int64_t items = 0;
-  for (int n = 1; n <= rows; ++n)
-    items = std::max<int64_t>(items, split_target(n, kv_head_num, table_stride, block_size) + n);
+  for (int n = 1; n <= std::min(rows, kAttnSplitMaxRows); ++n) {
+    const int t = split_target(n, kv_head_num, table_stride, block_size);
+    if (t > 0) items = std::max<int64_t>(items, t + n);
+  }
+  if (items == 0) return 0;
   const int64_t units = static_cast<int64_t>(rows) * kv_head_num;
   return static_cast<size_t>(ticket_bytes(units) + items * kv_head_num * G * (head_size + 2) * 4);
 }

@@ -101,6 +101,8 @@ def test_split_kv_workspace_bytes(sq8):
     assert f(64, 32, 8, 128, 68, 16) == 2048 + (96 + 63) * 8 * 4 * 130 * 4
     assert f(1, 28, 4, 64, 300, 4) == 256 + (192 + 1) * 4 * 7 * 66 * 4
     assert f(3, 32, 8, 128, 68, 16) < f(4, 32, 8, 128, 68, 16)
+    # total positions beyond 32 bits: 4096 rows never split, but calls of fewer rows may
+    assert f(4096, 32, 8, 128, 4000, 256) >= f(2097, 32, 8, 128, 4000, 256) > 0
 
 
 @pytest.mark.gpu
