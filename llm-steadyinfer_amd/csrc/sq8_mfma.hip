@@ -1573,7 +1573,10 @@ Plan make_plan(int M, int N, int K) {
   // Decode GEMM for wide outputs at 33-64 tokens (Llama gate/up at 48 and 64 rows: 59 and 63 us
   // against 70 and 77 for the tile kernel, which stays ahead on narrower outputs, where the
   // decode GEMM needs a deep K split to fill the GPU).
-  if (M > 32 && M <= 64 && N >= 16384) {
+  // 17-32 tokens on wide outputs up to 64Ki columns take it too (Llama gate/up at 24 and 32
+  // rows: 53.4 and 53.7 us against 56.6 and 56.3; the 128256-column LM head stays on the tile
+  // kernel, 209 against 217 us at 24 rows, as do 16 or fewer rows, 47.5 against 50.2).
+  if (M <= 64 && N >= 16384 && (M > 32 || (M > 16 && N <= 65536))) {
     p.dgemm = true;
     p.rt = rt;
     const int tiles = (N + kDgCols - 1) / kDgCols;

@@ -38,7 +38,7 @@ def to_dev(dev, *arrs):
 # after the product, and the decode GEMM (33-64 rows, wide outputs), which fuses it.
 SWIGLU_CASES = [(65, 256, 1024), (128, 200, 4096), (300, 512, 256), (2048, 128, 1024),
                 (1, 384, 1024), (4, 160, 2048), (8, 256, 4096), (16, 512, 1024), (33, 96, 8192),
-                (48, 8200, 1024), (64, 8192, 512)]
+                (48, 8200, 1024), (64, 8192, 512), (24, 8200, 1024)]
 
 
 @pytest.mark.parametrize("M,F,K", SWIGLU_CASES)

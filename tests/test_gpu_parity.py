@@ -212,9 +212,11 @@ def test_gemm_64_row_tiles(sq8, dev, M, N, K, gs):
 
 
 @pytest.mark.parametrize("M,N,K,gs", [(33, 16640, 1024, 64), (40, 16400, 2048, 128),
-                                      (48, 16384, 4096, 64), (64, 17000, 512, 64)])
+                                      (48, 16384, 4096, 64), (64, 17000, 512, 64),
+                                      (17, 16400, 1024, 64), (24, 28672, 1024, 64),
+                                      (32, 20000, 2048, 128)])
 def test_decode_gemm_wide_outputs(sq8, dev, M, N, K, gs):
-    """33-64 token rows on wide outputs take the decode GEMM (register weight ring, activation
+    """17-64 token rows on wide outputs take the decode GEMM (register weight ring, activation
     fragments shared through LDS): K split over several workgroups, ragged last column tiles,
     group size 128, and a split shorter than the ring."""
     x, q, s = o.make_case(M, N, K, gs, seed=M * 3 + N + K)

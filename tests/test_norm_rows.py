@@ -38,7 +38,8 @@ CASES = [(9, 512, 1024, "none", True), (20, 1024, 4096, "none", False),
          (64, 6144, 4096, "none", True), (40, 768, 2048, "none", True),
          (64, 16384, 1024, "swiglu", True), (48, 16400, 1024, "swiglu", False),
          (1, 512, 1024, "none", True), (100, 512, 1024, "none", True),
-         (100, 512, 1024, "swiglu", False), (16, 512, 1024, "swiglu", True)]
+         (100, 512, 1024, "swiglu", False), (16, 512, 1024, "swiglu", True),
+         (24, 16400, 1024, "swiglu", True)]
 
 
 @pytest.mark.gpu
