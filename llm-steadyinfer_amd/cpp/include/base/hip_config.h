@@ -15,7 +15,9 @@ struct HipConfig {
   // When true the destructor destroys `stream` (the reference's CudaConfig owns its stream).
   bool owns_stream = false;
 
-  // Returns a device workspace of at least `bytes` (nullptr when bytes == 0).
+  // Returns a device workspace of at least `bytes` (nullptr when bytes == 0). Returns nullptr,
+  // allocating nothing, when the workspace would have to grow while `stream` is capturing a
+  // graph: reserve_workspace() before the capture.
   void* workspace(size_t bytes);
   size_t workspace_bytes() const { return ws_bytes_; }
   // Grows the workspace now (outside any graph capture).

@@ -7,6 +7,13 @@ namespace kernel {
 void* HipConfig::workspace(size_t bytes) {
   if (bytes == 0) return ws_;
   if (bytes > ws_bytes_) {
+    // Growing means hipFree/hipMalloc and a zero fill: none of that may be recorded into a graph
+    // being captured on this stream, so refuse (nullptr) and leave the workspace as it is.
+    if (stream) {
+      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+        return nullptr;
+    }
     if (ws_) {
       // The old workspace may still be read by queued kernels on this stream.
       if (stream) CHECK(hipStreamSynchronize(stream) == hipSuccess);

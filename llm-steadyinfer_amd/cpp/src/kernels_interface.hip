@@ -24,6 +24,9 @@ void matmul_kernel_hip_qint8(const tensor::Tensor& input, const tensor::Tensor& 
   auto* cfg = const_cast<HipConfig*>(config);
   const size_t ws_bytes = sq8_workspace_bytes(M, N, K, group_size);
   void* ws = cfg->workspace(ws_bytes);
+  CHECK(ws_bytes == 0 || ws != nullptr)
+      << "sq8_matmul needs a " << ws_bytes << "-byte workspace, which cannot grow while the stream "
+      << "captures a graph (HipConfig::reserve_workspace before the capture)";
   const int rc = sq8_matmul(input.ptr<float>(), weight.ptr<int8_t>(), scale.ptr<float>(),
                             const_cast<float*>(output.ptr<float>()), M, N, K, group_size, ws,
                             cfg->workspace_bytes(), cfg->stream);

@@ -278,7 +278,7 @@ __global__ __launch_bounds__(W * kWave) void paged_attention_rows_kernel(
       for (int i = ln; i < rows; i += kWave) t += positions[i] + 1;
 #pragma unroll
       for (int d = 32; d >= 1; d >>= 1) t += __shfl_xor(t, d, kWave);
-      const int c = max(kAttnMinChunk, (t + n_target - 1) / n_target);
+      const int c = max(kAttnMinChunk, t / n_target + (t % n_target != 0));  // t may be INT_MAX
       int base = 0, sel = -1, sel_first = 0;
       for (int i0 = 0; i0 < rows; i0 += kWave) {
         const int i = i0 + ln;
@@ -612,8 +612,13 @@ int split_target(int rows, int kv_head_num, int table_stride, int block_size) {
   const int fill = units < kAttnFillUnits ? (kAttnFillItems + kv_head_num - 1) / kv_head_num : 0;
   return max(max(fill, rows / kAttnBalanceDiv), 1);
 }
-// Ticket area at the start of the split-KV workspace (one per (row, kv head), 256-byte aligned).
-int64_t ticket_bytes(int64_t units) { return (units * 4 + 255) / 256 * 256; }
+// Ticket area at the start of the split-KV workspace: one per (row, kv head) for every row count
+// that can split, 256-byte aligned. Its size depends on kv_head_num only, so calls of different
+// row counts sharing one workspace agree on where the tickets end and the partials begin (a
+// smaller call's partials never land on a larger call's tickets).
+int64_t ticket_bytes(int kv_head_num) {
+  return (static_cast<int64_t>(kAttnSplitMaxRows) * kv_head_num * 4 + 255) / 256 * 256;
+}
 
 }  // namespace
 }  // namespace sq8
@@ -662,8 +667,8 @@ size_t sq8_paged_attention_workspace_bytes(int rows, int head_num, int kv_head_n
     if (t > 0) items = std::max<int64_t>(items, t + n);
   }
   if (items == 0) return 0;
-  const int64_t units = static_cast<int64_t>(rows) * kv_head_num;
-  return static_cast<size_t>(ticket_bytes(units) + items * kv_head_num * G * (head_size + 2) * 4);
+  return static_cast<size_t>(ticket_bytes(kv_head_num) +
+                             items * kv_head_num * G * (head_size + 2) * 4);
 }
 
 int sq8_paged_attention_ws(const float* qkv, int q_stride, int rows, int head_num,
@@ -694,7 +699,7 @@ int sq8_paged_attention_ws(const float* qkv, int q_stride, int rows, int head_nu
     const int target = split ? split_target(rows, kv_head_num, table_stride, block_size) : 0;
     unsigned* tickets = split ? static_cast<unsigned*>(workspace) : nullptr;
     float* part = split ? reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                                   ticket_bytes(units))
+                                                   ticket_bytes(kv_head_num))
                         : nullptr;
     const dim3 grid((rows + target) * kv_head_num), block((wide ? 8 : 4) * kWave);
     const auto rk = [&](auto kernel) {

@@ -72,8 +72,13 @@ class Int8Decoder:
     @classmethod
     def from_file(cls, path, max_seq: int, device="cuda", fused: bool = True) -> "Int8Decoder":
         """Load an INT8 model file (reference layout) and upload fused projections."""
+        return cls.from_model(ModelFile(path), max_seq, device, fused)
+
+    @classmethod
+    def from_model(cls, m, max_seq: int, device="cuda", fused: bool = True) -> "Int8Decoder":
+        """Upload fused projections from a host model with ModelFile's accessors (a ModelFile or
+        a model_file.RandomModel)."""
         import torch
-        m = ModelFile(path)
         cfg, gs = m.config, m.group_size
 
         def dev(a, dtype):

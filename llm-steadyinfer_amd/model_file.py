@@ -155,42 +155,86 @@ def _row_step(rows: int, cols: int, group_size: int, rows_per_chunk: int) -> int
     return max(align, (min(rows, rows_per_chunk) // align) * align)
 
 
+def _random_blocks(cfg: ModelConfig, group_size: int, seed: int, w_std: float,
+                   rows_per_chunk: int):
+    """The random-init tensors in file order, in row chunks: yields (entry, first row, q, s) for
+    quantised chunks and (entry, first row, fp32 rows, None) for fp32 ones. Projection weights
+    ~ N(0, w_std) quantised per group, embedding ~ N(0, 1), RMSNorm weights 1; each tensor has
+    its own generator, so the values do not depend on how they are consumed."""
+    for e in layout(cfg, group_size):
+        rng = _block_rng(seed, e.name, e.layer)
+        if e.quantised:
+            if e.name == "cls" and cfg.shared:
+                continue  # the tied classifier has no bytes of its own (reference quirk)
+            step = _row_step(e.rows, e.cols, group_size, rows_per_chunk)
+            for r0 in range(0, e.rows, step):
+                r1 = min(e.rows, r0 + step)
+                wchunk = (rng.standard_normal((r1 - r0, e.cols), dtype=np.float32)
+                          * np.float32(w_std))
+                q, sc = quantize(wchunk, group_size)
+                yield e, r0, q, sc
+        elif e.name == "embedding":
+            for r0 in range(0, e.rows, rows_per_chunk):
+                r1 = min(e.rows, r0 + rows_per_chunk)
+                yield e, r0, rng.standard_normal((r1 - r0, e.cols), dtype=np.float32), None
+        else:
+            yield e, 0, np.ones((1, e.cols), np.float32), None
+
+
 def write_random(path, cfg: ModelConfig, group_size: int = 64, seed: int = 0,
                  w_std: float = 0.02, rows_per_chunk: int = 4096) -> Path:
     """Write a random-init INT8 model file: projection weights ~ N(0, w_std) quantised per group,
     embedding ~ N(0, 1), RMSNorm weights 1. Streams row chunks, so memory stays bounded for the
     Llama-3-8B shapes. Deterministic in ``seed``."""
     path = Path(path)
-    ents = layout(cfg, group_size)
     base = HEADER_BYTES + 4
     with open(path, "wb") as f:
         f.write(cfg.pack())
         f.write(struct.pack(GROUP_FMT, group_size))
         f.truncate(file_bytes(cfg, group_size))
-        for e in ents:
-            rng = _block_rng(seed, e.name, e.layer)
-            if e.quantised:
-                if e.name == "cls" and cfg.shared:
-                    continue  # the tied classifier has no bytes of its own (reference quirk)
-                step = _row_step(e.rows, e.cols, group_size, rows_per_chunk)
-                for r0 in range(0, e.rows, step):
-                    r1 = min(e.rows, r0 + step)
-                    wchunk = (rng.standard_normal((r1 - r0, e.cols), dtype=np.float32)
-                              * np.float32(w_std))
-                    q, s = quantize(wchunk, group_size)
-                    f.seek(base + e.offset + r0 * e.cols)
-                    f.write(q.tobytes())
-                    f.seek(base + e.scale_offset + (r0 * e.cols // group_size) * 4)
-                    f.write(s.tobytes())
-            elif e.name == "embedding":
-                for r0 in range(0, e.rows, rows_per_chunk):
-                    r1 = min(e.rows, r0 + rows_per_chunk)
-                    f.seek(base + e.offset + r0 * e.cols * 4)
-                    f.write(rng.standard_normal((r1 - r0, e.cols), dtype=np.float32).tobytes())
+        for e, r0, a, sc in _random_blocks(cfg, group_size, seed, w_std, rows_per_chunk):
+            if sc is not None:
+                f.seek(base + e.offset + r0 * e.cols)
+                f.write(a.tobytes())
+                f.seek(base + e.scale_offset + (r0 * e.cols // group_size) * 4)
+                f.write(sc.tobytes())
             else:
-                f.seek(base + e.offset)
-                f.write(np.ones(e.cols, np.float32).tobytes())
+                f.seek(base + e.offset + r0 * e.cols * 4)
+                f.write(a.tobytes())
     return path
+
+
+class RandomModel:
+    """The model ``write_random`` would write with the same arguments, held in host memory with
+    ModelFile's accessors (config, group_size, quant, fp32): for tests and benchmarks at full
+    widths without the file round trip. Bit-identical to reading the written file."""
+
+    def __init__(self, cfg: ModelConfig, group_size: int = 64, seed: int = 0,
+                 w_std: float = 0.02, rows_per_chunk: int = 4096):
+        self.config, self.group_size = cfg, group_size
+        self._q, self._f = {}, {}
+        for e, r0, a, sc in _random_blocks(cfg, group_size, seed, w_std, rows_per_chunk):
+            key = (e.name, e.layer)
+            if sc is not None:
+                if key not in self._q:
+                    self._q[key] = (np.empty((e.rows, e.cols), np.int8),
+                                    np.empty(e.rows * e.cols // group_size, np.float32))
+                q, s = self._q[key]
+                q.reshape(-1)[r0 * e.cols:r0 * e.cols + a.size] = a
+                s0 = r0 * e.cols // group_size
+                s[s0:s0 + sc.size] = sc
+            else:
+                if key not in self._f:
+                    self._f[key] = np.empty((e.rows, e.cols), np.float32)
+                self._f[key][r0:r0 + a.shape[0]] = a
+        if cfg.shared:  # the reference binds the tied classifier at the embedding's bytes
+            raise ValueError("RandomModel holds untied models only (negative vocab_size)")
+
+    def quant(self, name: str, layer: int = 0):
+        return self._q[(name, layer)]
+
+    def fp32(self, name: str, layer: int = 0) -> np.ndarray:
+        return self._f[(name, layer)]
 
 
 def regenerate_block(cfg: ModelConfig, group_size: int, name: str, layer: int, seed: int = 0,

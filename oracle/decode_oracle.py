@@ -64,6 +64,28 @@ def attention(q, kcache, vcache, pos: int, head_num: int, kv_head_num: int, head
     return out.reshape(-1)
 
 
+def attention_causal(q, kcache, vcache, pos0: int, head_num: int, kv_head_num: int,
+                     head_size: int):
+    """attention() for T query rows at positions pos0 .. pos0+T-1 (q: [T, head_num*head_size]):
+    row i attends to cache rows 0 .. pos0+i, the paged kernels' causal rule for prefill rows of
+    one sequence (paged_kernels.cu:96-294)."""
+    q = np.asarray(q, np.float64)
+    T = q.shape[0]
+    q = q.reshape(T, head_num, head_size)
+    n = pos0 + T
+    out = np.empty((T, head_num, head_size))
+    mask = np.arange(n)[None, :] > (pos0 + np.arange(T))[:, None]
+    for h in range(head_num):
+        g = h * kv_head_num // head_num
+        k = np.asarray(kcache[:n, g * head_size:(g + 1) * head_size], np.float64)
+        v = np.asarray(vcache[:n, g * head_size:(g + 1) * head_size], np.float64)
+        s = q[:, h] @ k.T / np.sqrt(head_size)
+        s[mask] = -np.inf
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        out[:, h] = (p @ v) / p.sum(axis=1, keepdims=True)
+    return out.reshape(T, -1)
+
+
 def swiglu(a, b):
     """swiglu_kernel_cu_fp32 (swiglu_kernel.cu:4-21): a * sigmoid(a) * b."""
     a = np.asarray(a, np.float64)
@@ -76,10 +98,18 @@ def argmax_first(logits) -> int:
 
 
 def dequant(q, s, group_size: int):
-    """w[n][k] = (float)q[n][k] * scale of its group, formed in fp32 (matmul_kernel.cu:85-88)."""
+    """w[n][k] = (float)q[n][k] * scale of its group, formed in fp32 (matmul_kernel.cu:85-88).
+    Works through row blocks (whole groups) so the fp32 temporaries stay cache-sized."""
     q = np.asarray(q)
-    w = q.reshape(-1, group_size).astype(np.float32) * np.asarray(s, np.float32)[:, None]
-    return w.reshape(q.shape).astype(np.float64)
+    s = np.asarray(s, np.float32)
+    flat = q.reshape(-1)
+    out = np.empty(flat.size, np.float64)
+    step = group_size * 65536
+    for a in range(0, flat.size, step):
+        blk = flat[a:a + step].reshape(-1, group_size).astype(np.float32)
+        g0 = a // group_size
+        out[a:a + blk.size] = (blk * s[g0:g0 + blk.shape[0], None]).reshape(-1)
+    return out.reshape(q.shape)
 
 
 class DecodeModel:
@@ -123,13 +153,44 @@ class DecodeModel:
             return None
         return self.cls @ rmsnorm(x, self.norm[2 * L])
 
-    def generate(self, prompt, n_new: int):
-        """Prompt tokens one at a time without logits, then greedy tokens (the reference's
-        predict(is_prompt) loop). Returns the generated tokens and every step's logits."""
+    def prefill(self, tokens, pos0: int = 0):
+        """Positions pos0 .. pos0+T-1 of tokens in one pass: the same per-position arithmetic as
+        T calls of step(want_logits=False) (row-independent projections, norms and RoPE), with
+        each position attending causally to cache rows 0..its own position. Matrix products over
+        the T rows make long prompts affordable in float64."""
+        cfg, L = self.cfg, self.cfg.layer_num
+        T = len(tokens)
+        if T == 0:
+            return
+        pos = np.arange(pos0, pos0 + T)
+        x = self.emb[np.asarray(tokens, np.int64)].copy()
+        hs, H, KV = self.hs, cfg.head_num, cfg.kv_head_num
+        for l in range(L):
+            xn = rmsnorm(x, self.norm[l])
+            q = xn @ self.W[("wq", l)].T
+            k = xn @ self.W[("wk", l)].T
+            v = xn @ self.W[("wv", l)].T
+            q = np.stack([rope(q[i], H, hs, p, self.sin, self.cos) for i, p in enumerate(pos)])
+            k = np.stack([rope(k[i], KV, hs, p, self.sin, self.cos) for i, p in enumerate(pos)])
+            self.K[l, pos0:pos0 + T], self.V[l, pos0:pos0 + T] = k, v
+            a = attention_causal(q, self.K[l], self.V[l], pos0, H, KV, hs)
+            x = x + a @ self.W[("wo", l)].T
+            xn = rmsnorm(x, self.norm[L + l])
+            h = swiglu(xn @ self.W[("w1", l)].T, xn @ self.W[("w3", l)].T)
+            x = x + h @ self.W[("w2", l)].T
+
+    def generate(self, prompt, n_new: int, batched_prompt: bool = False):
+        """Prompt tokens one at a time without logits (or all at once through prefill() when
+        batched_prompt), then greedy tokens (the reference's predict(is_prompt) loop). Returns
+        the generated tokens and every step's logits."""
         pos = 0
-        for t in prompt[:-1]:
-            self.step(int(t), pos, want_logits=False)
-            pos += 1
+        if batched_prompt:
+            self.prefill([int(t) for t in prompt[:-1]])
+            pos = len(prompt) - 1
+        else:
+            for t in prompt[:-1]:
+                self.step(int(t), pos, want_logits=False)
+                pos += 1
         tok = int(prompt[-1])
         out, logits = [], []
         for _ in range(n_new):

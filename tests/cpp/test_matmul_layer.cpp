@@ -137,6 +137,27 @@ void run_case(int M, int N, int K, int gs, bool one_d, bool with_bias) {
   if (!ok) ++sq8test::failures();
 }
 
+// A workspace that would have to grow while its stream captures a graph is refused (nullptr, no
+// allocation, the old workspace kept); after the capture ends it grows as usual.
+void test_workspace_refused_while_capturing() {
+  kernel::HipConfig cfg;
+  EXPECT(hipStreamCreate(&cfg.stream) == hipSuccess, "stream");
+  cfg.owns_stream = true;
+  void* small = cfg.workspace(4096);
+  EXPECT(small != nullptr && cfg.workspace_bytes() == 4096, "first workspace");
+  EXPECT(hipStreamBeginCapture(cfg.stream, hipStreamCaptureModeRelaxed) == hipSuccess,
+         "begin capture");
+  EXPECT(cfg.workspace(1 << 20) == nullptr, "growth refused while capturing");
+  EXPECT(cfg.workspace_bytes() == 4096, "workspace unchanged while capturing");
+  EXPECT(cfg.workspace(1024) == small, "a size that fits is served while capturing");
+  hipGraph_t graph = nullptr;
+  EXPECT(hipStreamEndCapture(cfg.stream, &graph) == hipSuccess, "end capture");
+  if (graph) (void)hipGraphDestroy(graph);
+  EXPECT(cfg.workspace(1 << 20) != nullptr && cfg.workspace_bytes() == (1u << 20),
+         "growth after the capture");
+  EXPECT(hipStreamSynchronize(cfg.stream) == hipSuccess, "sync");
+}
+
 void test_gpu() {
   run_case(1, 4096, 4096, 64, /*one_d=*/true, false);   // single-token forward() path
   run_case(1, 1000, 1536, 64, false, false);
@@ -148,6 +169,7 @@ void test_gpu() {
   // The workspace is reused across layers of different shapes (zero tickets are preserved).
   run_case(8, 4096, 4096, 64, false, false);
   run_case(8, 28672, 4096, 64, false, false);
+  test_workspace_refused_while_capturing();
 }
 
 }  // namespace

@@ -88,18 +88,20 @@ def test_paged_attention_matches_oracle(sq8, dev, heads, kv_heads, hs, block_siz
 
 def test_split_kv_workspace_bytes(sq8):
     """Split-KV workspace: none when a table row spans at most 128 positions, the row kernel does
-    not cover the head shape or the table row does not fit its LDS; otherwise 256-byte-aligned
-    tickets per (row, kv head) plus G * (head_size + 2) floats per (work item, kv head), with
+    not cover the head shape or the table row does not fit its LDS; otherwise a ticket area of
+    4096 rows x kv_head_num tickets (the same for every row count, so calls of different sizes
+    on one workspace agree on where the partials start) plus G * (head_size + 2) floats per
+    (work item, kv head), with
     768 / kv_head_num work items (fewer than 512 row-kv-head pairs) or rows, plus rows, at
     most over every row count up to rows."""
     f = sq8.paged_attention_workspace_bytes
     assert f(8, 32, 8, 128, 8, 16) == 0             # 128 positions: never split
     assert f(8, 32, 8, 256, 64, 16) == 0            # head_size 256: generic kernel
     assert f(8, 32, 8, 128, 4096, 16) == 0          # table row beyond the LDS stage
-    assert f(8, 32, 8, 128, 16, 16) == 256 + (96 + 8) * 8 * 4 * 130 * 4
+    assert f(8, 32, 8, 128, 16, 16) == 4096 * 8 * 4 + (96 + 8) * 8 * 4 * 130 * 4
     # 64 rows: 64 + 64 items; 63 rows (504 pairs): 96 + 63, the most for up to 64 rows
-    assert f(64, 32, 8, 128, 68, 16) == 2048 + (96 + 63) * 8 * 4 * 130 * 4
-    assert f(1, 28, 4, 64, 300, 4) == 256 + (192 + 1) * 4 * 7 * 66 * 4
+    assert f(64, 32, 8, 128, 68, 16) == 4096 * 8 * 4 + (96 + 63) * 8 * 4 * 130 * 4
+    assert f(1, 28, 4, 64, 300, 4) == 4096 * 4 * 4 + (192 + 1) * 4 * 7 * 66 * 4
     assert f(3, 32, 8, 128, 68, 16) < f(4, 32, 8, 128, 68, 16)
     # total positions beyond 32 bits: 4096 rows never split, but calls of fewer rows may
     assert f(4096, 32, 8, 128, 4000, 256) >= f(2097, 32, 8, 128, 4000, 256) > 0
@@ -140,7 +142,43 @@ def test_split_kv_attention_matches_oracle(sq8, dev, heads, kv_heads, hs, block_
             ref = do.attention(qkv[i, :dim], K[s], V[s], p, heads, kv_heads, hs)
             err = np.max(np.abs(got[i] - ref)) / max(np.max(np.abs(ref)), 1e-30)
             assert err < 2e-6, (rows, i, s, p, err)
-        assert int(ws[:tab.shape[0] * kv_heads].abs().sum()) == 0  # tickets back at zero
+        assert int(ws[:4096 * kv_heads].abs().sum()) == 0  # tickets back at zero
+
+
+@pytest.mark.gpu
+def test_split_kv_small_call_then_large_call(sq8, dev):
+    """One workspace shared by calls of different row counts: a 2-row call whose long row
+    splits (its partials are written), then a 24-row call (24 x 8 kv heads > 64 tickets) whose
+    rows split too, then the small call again. A partial area that moved with the call's row
+    count would put the small call's partials on the large call's tickets; every output must
+    match the oracle and the whole ticket area must be zero after each call."""
+    import torch
+    heads, kv_heads, hs, block_size = 32, 8, 128, 16
+    rng = np.random.default_rng(2024)
+    lens = [1200, 900, 700, 650, 30]
+    kv = kv_heads * hs
+    kc, vc, tables, K, V = _paged_case(rng, lens, kv, block_size, extra_blocks=3)
+    dim = heads * hs
+    stride = dim + 2 * kv
+    width = len(tables[0])
+    ws = torch.zeros((sq8.paged_attention_workspace_bytes(
+        64, heads, kv_heads, hs, width, block_size) + 3) // 4, dtype=torch.int32, device=dev)
+    kc_t, vc_t = _t(kc, dev), _t(vc, dev)
+    small = [(0, 1199), (4, 29)]
+    large = [(int(s), int(rng.integers(400, lens[s]))) for s in rng.integers(0, 4, 24)]
+    for rows in (small, large, small, large):
+        qkv = rng.standard_normal((len(rows), stride)).astype(np.float32)
+        pos = np.array([p for _, p in rows], np.int32)
+        tab = np.array([tables[s] for s, _ in rows], np.int32)
+        out = torch.full((len(rows), dim), float("nan"), device=dev)
+        sq8.paged_attention(_t(qkv, dev), stride, heads, kv_heads, hs, _t(pos, dev),
+                            _t(tab, dev), block_size, kc_t, vc_t, out, workspace=ws)
+        got = out.cpu().numpy()
+        for i, (s, p) in enumerate(rows):
+            ref = do.attention(qkv[i, :dim], K[s], V[s], p, heads, kv_heads, hs)
+            err = np.max(np.abs(got[i] - ref)) / max(np.max(np.abs(ref)), 1e-30)
+            assert err < 2e-6, (len(rows), i, s, p, err)
+        assert int(ws[:4096 * kv_heads].abs().sum()) == 0
 
 
 @pytest.mark.gpu

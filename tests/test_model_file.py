@@ -102,6 +102,25 @@ def test_write_then_read(tmp_path, cfg, gs):
     assert emb.shape == (cfg.vocab, cfg.dim) and abs(float(emb.std()) - 1.0) < 0.05
 
 
+@pytest.mark.parametrize("gs", [64, 32])
+def test_random_model_equals_written_file(tmp_path, gs):
+    """RandomModel (in memory) holds exactly the bytes write_random puts in the file."""
+    path = mf.write_random(tmp_path / "m.bin", TINY, gs, seed=3, rows_per_chunk=96)
+    m, r = mf.ModelFile(path), mf.RandomModel(TINY, gs, seed=3, rows_per_chunk=96)
+    assert r.config == m.config and r.group_size == m.group_size
+    for name in mf.QUANT_ORDER:
+        for layer in range(TINY.layer_num):
+            for a, b in zip(r.quant(name, layer), m.quant(name, layer)):
+                np.testing.assert_array_equal(a, b)
+    for a, b in zip(r.quant("cls"), m.quant("cls")):
+        np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(r.fp32("embedding"), m.fp32("embedding"))
+    for i in range(2 * TINY.layer_num + 1):
+        np.testing.assert_array_equal(r.fp32("rmsnorm", i), m.fp32("rmsnorm", i))
+    with pytest.raises(ValueError):
+        mf.RandomModel(TINY_TIED, 64)
+
+
 @pytest.mark.parametrize("cfg", [TINY, TINY_TIED])
 def test_cpp_loader_offsets_match_layout(tmp_path, cfg):
     """The C++ loader (Int8ModelFile) binds every tensor at the offset the layout predicts."""
