@@ -95,6 +95,22 @@ size_t sq8_rmsnorm_rows_workspace_bytes(int M, int N, int K, int group_size, int
 /* 1 if sq8_matmul_epilogue fuses the epilogue into the matmul kernel for this shape, else 0. */
 int sq8_epilogue_fused(int M, int N, int K, int group_size);
 
+/* Size of the device scratch array behind sq8_matmul_noalloc (32 MiB per GPU). */
+#define SQ8_NOALLOC_SCRATCH_BYTES (32u * 1024u * 1024u)
+
+/* sq8_matmul without a workspace argument and without any allocation: no counterpart in the
+ * reference (whose kernel needs no workspace); for callers that cannot allocate device memory
+ * (code under graph capture, tight serving loops, harnesses that forbid hipMalloc). The
+ * workspace is a fixed device array of SQ8_NOALLOC_SCRATCH_BYTES in the library, one per GPU,
+ * held until the process ends; the first call on a device looks up its address and clears its
+ * ticket area (a kernel on hip_stream). Shapes whose sq8_workspace_bytes() exceeds it return
+ * SQ8_ERR_WORKSPACE (every Llama-3-8B projection up to 64 token rows fits). All calls on one
+ * GPU share the array: calls that overlap in time on one GPU (other streams, other threads)
+ * race and must not be issued. Results are bitwise those of sq8_matmul. */
+int sq8_matmul_noalloc(const float* x, const int8_t* w, const float* scales, float* y, int M,
+                       int N, int K, int group_size, void* hip_stream);
+size_t sq8_noalloc_scratch_bytes(void);
+
 /* Human-readable text of a status code. */
 const char* sq8_status_string(int status);
 

@@ -24,7 +24,8 @@ SQ8_ERR_DEVICE = -6
 EXPORTED_SYMBOLS = ("sq8_matmul", "sq8_workspace_bytes", "sq8_status_string", "sq8_path_name",
                     "sq8_matmul_epilogue", "sq8_epilogue_workspace_bytes", "sq8_epilogue_fused",
                     "sq8_matmul_rmsnorm_rows", "sq8_rmsnorm_rows_fused",
-                    "sq8_rmsnorm_rows_workspace_bytes")
+                    "sq8_rmsnorm_rows_workspace_bytes", "sq8_matmul_noalloc",
+                    "sq8_noalloc_scratch_bytes")
 
 # Output epilogues (include/sq8.h, enum sq8_epilogue).
 SQ8_EPI_NONE = 0
@@ -99,11 +100,14 @@ def lib() -> ctypes.CDLL:
             "sq8_paged_attention_ws": [vp, I, I, I, I, I, vp, vp, I, I, vp, vp, vp, vp, sz, vp],
             "sq8_swiglu_rows": [vp, I, I, vp, vp],
             "sq8_argmax_rows": [vp, I, I, vp, vp],
+            "sq8_matmul_noalloc": [vp, vp, vp, vp, I, I, I, I, vp],
         }
         for name, args in sigs.items():
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = I
+        L.sq8_noalloc_scratch_bytes.argtypes = []
+        L.sq8_noalloc_scratch_bytes.restype = sz
         L.sq8_argmax_workspace_bytes.argtypes = [I]
         L.sq8_argmax_workspace_bytes.restype = sz
         L.sq8_paged_attention_workspace_bytes.argtypes = [I, I, I, I, I, I]
