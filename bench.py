@@ -152,6 +152,7 @@ def decode_run(torch, n_prompt: int = 64, n_new: int = 128, seed: int = 0):
         D.token.fill_(int(t))
         D._launch_step(st, want_logits=False)
     D.token.fill_(int(prompt[-1]))
+    D.begin_decode(st)
     torch.cuda.synchronize()
     prompt_ms = (time.perf_counter() - t0) * 1e3
     toks = torch.empty(n_new, dtype=torch.int32, device=D.device)
@@ -171,6 +172,112 @@ def decode_run(torch, n_prompt: int = 64, n_new: int = 128, seed: int = 0):
             "prompt_ms_eager": round(prompt_ms, 1), "weight_bytes_per_token": wb,
             "weight_GBps": round(wb / ms / 1e6, 1), "launch": "hip_graph per token",
             "first_tokens": toks[:8].cpu().tolist()}
+
+
+def llama_decode_run(torch, weights, lm_head, n_prompt: int = 64, n_new: int = 128,
+                     seed: int = 0):
+    """Batch-1 greedy decode on the Llama-3-8B-shaped INT8 model (the step's random-init
+    projections, a random embedding, unit norms) through the HIP decode stack (decoder.py: the
+    reference's single-token LLamaModel::predict / forward, llama3.cpp:705-818), one HIP-graph
+    replay per token, timed with HIP events; the 64-token prompt runs eagerly, untimed."""
+    import importlib
+    import numpy as np
+    mf = importlib.import_module("llm_steadyinfer_amd.model_file")
+    dec = importlib.import_module("llm_steadyinfer_amd.decoder")
+    cfg = mf.LLAMA3_8B
+    dev = lm_head[0].device
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed + 99)
+    w = {"qkv": weights["qkv"], "o": weights["o"], "gu": weights["gate_up"],
+         "down": weights["down"], "cls": lm_head,
+         "emb": torch.randn((cfg.vocab, cfg.dim), generator=gen, device=dev),
+         "norm": [torch.ones(cfg.dim, device=dev) for _ in range(2 * cfg.layer_num + 1)]}
+    D = dec.Int8Decoder(cfg, w, GS, n_prompt + n_new, device=dev)
+    prompt = np.random.default_rng(seed).integers(0, cfg.vocab, n_prompt).tolist()
+    D.generate(prompt, 4)                      # captures the graph, warms every kernel
+    st = torch.cuda.current_stream()
+    D.reset()
+    for t in prompt[:-1]:
+        D.token.fill_(int(t))
+        D._launch_step(st, want_logits=False)
+    D.token.fill_(int(prompt[-1]))
+    D.begin_decode(st)
+    toks = torch.empty(n_new, dtype=torch.int32, device=dev)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for i in range(n_new):
+        D.graph.replay()
+        toks[i:i + 1].copy_(D.token)
+    b.record(st)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / n_new
+    wb = D.weight_bytes()
+    return {"workload": "Llama-3-8B-shaped random-init INT8 model (32 layers, hidden 4096, 32/8 "
+                        "heads, FFN 14336, vocab 128256, group 64), batch 1, "
+                        f"{n_prompt}-token prompt, {n_new} greedy tokens",
+            "tokens_per_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4),
+            "weight_bytes_per_token": wb, "weight_GBps": round(wb / ms / 1e6, 1),
+            "frac_of_hbm_peak": round(wb / ms / 1e6 / HBM_PEAK_GBS, 4),
+            "launch": "hip_graph per token", "first_tokens": toks[:8].cpu().tolist()}
+
+
+def read_ceiling(torch, sq8, dev, shapes):
+    """The read-only streaming probe (include/sq8_probe.h) over as many bytes as each shape's M=1
+    GEMV reads, back to back over buffers rotated through > 1 GB, at a few grid and load-depth
+    settings; the fastest setting is the ceiling a kernel reading those bytes once can reach."""
+    out = {}
+    sink = torch.zeros(4096, dtype=torch.int32, device=dev)
+    for name, nbytes in shapes:
+        n = (nbytes + 255) // 256 * 256
+        nbuf = max(2, min(16, (1 << 30) // n + 1))
+        bufs = [torch.empty(n, dtype=torch.uint8, device=dev) for _ in range(nbuf)]
+        best = None
+        fn = sq8.lib().sq8_probe_stream_read
+        st = torch.cuda.current_stream().cuda_stream
+        for wpc, u in ((4, 4), (8, 4), (8, 2), (16, 2), (4, 8), (2, 8), (16, 4), (32, 1)):
+            args = [(b.data_ptr(), n, sink.data_ptr(), sink.numel(), wpc, u, st) for b in bufs]
+            for a_ in args:
+                fn(*a_)
+            reps = 4 * nbuf
+            a, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for i in range(reps):
+                fn(*args[i % nbuf])
+            e.record()
+            torch.cuda.synchronize()
+            us = a.elapsed_time(e) * 1e3 / reps
+            if best is None or us < best[0]:
+                best = (us, wpc, u)
+        out[name] = {"bytes": n, "us": round(best[0], 2), "GB/s": round(n / best[0] / 1e3, 1),
+                     "workgroups_per_cu": best[1], "chunks_per_lane": best[2]}
+        del bufs
+    return out
+
+
+def copy_ceiling(torch, dev, shapes):
+    """Device-to-device copies moving as many HBM bytes (read + write) as each shape's M=1 GEMV
+    reads, back to back over buffers rotated through > 1 GB (so the 256 MB Infinity Cache cannot
+    serve them): the box's streaming ceiling at that transfer size, launch floor included."""
+    out = {}
+    for name, nbytes in shapes:
+        half = (nbytes // 2 + 255) // 256 * 256
+        nbuf = max(2, min(16, (1 << 30) // half + 1))
+        src = [torch.empty(half, dtype=torch.uint8, device=dev) for _ in range(nbuf)]
+        dst = [torch.empty(half, dtype=torch.uint8, device=dev) for _ in range(nbuf)]
+        for i in range(nbuf):
+            dst[i].copy_(src[i])
+        reps = 4 * nbuf
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(reps):
+            dst[i % nbuf].copy_(src[i % nbuf])
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / reps
+        out[name] = {"bytes_moved": 2 * half, "us": round(us, 2),
+                     "GB/s": round(2 * half / us / 1e3, 1)}
+        del src, dst
+    return out
 
 
 def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed: int = 0,
@@ -250,6 +357,11 @@ def main():
     ap.add_argument("--graph", action="store_true", help="replay the step as one HIP graph")
     ap.add_argument("--profile", action="store_true",
                     help="short run for counter collection: a 256 MiB copy, then 5 decode steps")
+    ap.add_argument("--profile-decode-gemm", action="store_true",
+                    help="short run for counter collection: the four projections at M = 8, 32 "
+                         "and 64 (configs 2), 3 launches each on distinct layers")
+    ap.add_argument("--no-llama-decode", action="store_true",
+                    help="skip the Llama-3-8B batch-1 end-to-end decode")
     ap.add_argument("--profile-prefill", action="store_true",
                     help="short run for counter collection: the four config-3 prefill GEMMs "
                          "(M = 2048), 3 launches each")
@@ -311,6 +423,20 @@ def main():
         print(json.dumps({"profile_run": "prefill", "M": 2048, "launches_per_shape": 3}))
         return
 
+    if args.profile_decode_gemm:
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        for M in (8, 32, 64):
+            for p, (N, K) in PROJ.items():
+                x, y = xbuf(M, K), torch.empty((M, N), device=dev)
+                for l in range(3):
+                    Call(sq8, x, *weights[p][l], y, stream, ws)()
+                torch.cuda.synchronize()
+        print(json.dumps({"profile_run": "decode_gemm", "M": [8, 32, 64],
+                          "launches_per_shape": 3}))
+        return
+
     if args.profile:
         # Calibration copy of known size for FETCH_SIZE / WRITE_SIZE, then a few decode steps.
         a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
@@ -355,7 +481,8 @@ def main():
         step()
     e1.record(stream)
     torch.cuda.synchronize()
-    launch_us = e0.elapsed_time(e1) * 1e3 / (reps * len(calls))
+    step_launch_us = e0.elapsed_time(e1) * 1e3 / (reps * len(calls))
+    launch_us = step_launch_us
     bytes_per_launch = step_bytes / len(calls)
     achieved = bytes_per_launch / launch_us / 1e3
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -364,6 +491,9 @@ def main():
                 "kernel": "sq8 sweep_kernel, M=1 decode GEMV (per-shape configurations: "
                           "csrc/sq8_gemv.hip launch_stream)",
                 "avg_launch_us": round(launch_us, 3),
+                "avg_launch_us_source": "HIP events around whole eager steps / launches (the "
+                                        "launches run back to back; the kernel trace in "
+                                        "profiles/ gives the per-kernel durations)",
                 "algo_bytes_per_launch": round(bytes_per_launch)}
 
     # ---------------------------------------------------------------- configs 2 and 3 sweep
@@ -409,6 +539,39 @@ def main():
                              "M=2048 over the four Llama-3-8B projections",
                    "us_per_layer": round(us, 1)}
 
+    # Streaming ceilings at each projection's size, against the GEMV's per-shape time (the M=1
+    # rows of the sweep: 32 back-to-back launches of the shape).
+    shape_bytes = [(p, algo_bytes(1, N, K)) for p, (N, K) in PROJ.items()] + \
+        [("lm_head", algo_bytes(1, VOCAB, HIDDEN))]
+    rceil = read_ceiling(torch, sq8, dev, shape_bytes)
+    cceil = copy_ceiling(torch, dev, shape_bytes)
+    gemv_us = {r["proj"]: r["us"] for r in sweep if r["M"] == 1}
+    counts = {p: LAYERS for p in PROJ}
+    counts["lm_head"] = 1
+    per_shape = {}
+    for p, nb in shape_bytes:
+        rec = {"algo_bytes": nb, "read_probe_us": rceil[p]["us"], "copy_us": cceil[p]["us"],
+               "read_probe_setting": [rceil[p]["workgroups_per_cu"],
+                                      rceil[p]["chunks_per_lane"]]}
+        if p in gemv_us:
+            rec["gemv_us"] = gemv_us[p]
+            rec["gemv_GBps"] = round(nb / gemv_us[p] / 1e3, 1)
+            rec["gemv_frac_of_peak"] = round(nb / gemv_us[p] / 1e3 / HBM_PEAK_GBS, 4)
+            rec["gemv_frac_of_read_probe"] = round(rceil[p]["us"] / gemv_us[p], 3)
+        per_shape[p] = rec
+    ceil_step_us = sum(rceil[p]["us"] * counts[p] for p in counts)
+    roofline["read_ceiling"] = {
+        "step_ms": round(ceil_step_us / 1e3, 4),
+        "frac_of_peak": round(step_bytes / ceil_step_us / 1e3 / HBM_PEAK_GBS, 4),
+        "note": "the step's 129 launches priced at the read-only probe's time for each size",
+        "per_shape": per_shape}
+
+    llama = None
+    if not args.no_llama_decode:
+        llama = llama_decode_run(torch, weights, lm_head)
+        print(f"# llama decode done: {llama['tokens_per_s']} tokens/s", file=sys.stderr,
+              flush=True)
+
     decode = None
     if not args.no_decode:
         decode = decode_run(torch)
@@ -436,6 +599,8 @@ def main():
         "launch": "hip_graph" if args.graph else "eager",
         "graph_GBps": round(step_bytes / dt_graph / 1e9, 1) if dt_graph else None,
         "decode_matmul_tokens_per_s": round(1.0 / dt, 1),
+        "llama_decode_tokens_per_s": llama["tokens_per_s"] if llama else None,
+        "llama_decode": llama,
         "decode_tokens_per_s": decode["tokens_per_s"] if decode else None,
         "decode": decode,
         "batch_output_tokens_per_s": batch["output_tokens_per_s"] if batch else None,

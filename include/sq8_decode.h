@@ -86,6 +86,15 @@ size_t sq8_argmax_workspace_bytes(int n);
 int sq8_argmax(const float* logits, int n, int32_t* out, void* workspace, size_t workspace_bytes,
                void* hip_stream);
 
+/* The end of a greedy decode step in one launch: *token = first argmax of logits[0..n) (as
+ * sq8_argmax, same workspace), *pos += 1, and x[0..dim) = emb_table[*token][0..dim) (the next
+ * step's input, emb_kernel_cu_fp32, emb_kernel.cu:3-21; a token outside [0, vocab) leaves x).
+ * Replaces the reference's host-side sampler loop (argmax_sampler.cpp:5-13, the position and
+ * token update of LLamaModel::predict, llama3.cpp:724) followed by the next step's embedding. */
+int sq8_argmax_advance(const float* logits, int n, void* workspace, size_t workspace_bytes,
+                       int32_t* pos, int32_t* token, const float* emb_table, int vocab, int dim,
+                       float* x, void* hip_stream);
+
 /* Fused decode projections: y[N] = matmul(x', w, scales) for one token row, where x' is formed
  * while the GEMV stages its input (no extra launch, no round trip through memory):
  *   sq8_matmul_rmsnorm: r = x + res (res may be NULL: r = x), x' = rmsnorm(r) * norm_w with the
@@ -93,6 +102,8 @@ int sq8_argmax(const float* logits, int n, int32_t* out, void* workspace, size_t
  *     Replaces the reference's add + RMSNorm + projection sequence (qwen2.cpp:780-800).
  *   sq8_matmul_swiglu: gate_up = [a (K) | b (K)], x' = silu(a) * b; replaces SwiGLU + w2
  *     (qwen2.cpp:800-815).
+ * The RMSNorm scale rsqrt(mean(r^2) + eps) is applied to the finished dot products (it is one
+ * scalar for the row), r * norm_w is what the GEMV stages.
  * Accepted shapes are those of the single-row GEMV: group_size % 16 == 0, K % group_size == 0,
  * 4*K bytes within the 64 KiB activation stage, 16-byte aligned vectors and weights; otherwise
  * SQ8_ERR_DIMS / SQ8_ERR_GROUP. No workspace. */
@@ -101,6 +112,16 @@ int sq8_matmul_rmsnorm(const float* x, const float* res, float* x_out, const flo
                        int group_size, void* hip_stream);
 int sq8_matmul_swiglu(const float* gate_up, const int8_t* w, const float* scales, float* y, int N,
                       int K, int group_size, void* hip_stream);
+
+/* The FFN input projection of a decode step in one launch: with x' = rmsnorm(x + res) * norm_w
+ * as in sq8_matmul_rmsnorm and the fused weight w = [w1; w3] (N = 2F rows, the F gate rows first,
+ * each row's scales with it), y[i] = silu(g_i) * u_i for i < F, g = x' . w1^T, u = x' . w3^T:
+ * the add, RMSNorm, w1 and w3 projections and SwiGLU of the reference (qwen2.cpp:780-805;
+ * swiglu_kernel.cu:4-21). One wave computes both rows of an output. N must be even; other
+ * conditions as sq8_matmul_rmsnorm. y holds N/2 values. */
+int sq8_matmul_rmsnorm_swiglu(const float* x, const float* res, float* x_out, const float* norm_w,
+                              float eps, const int8_t* w, const float* scales, float* y, int N,
+                              int K, int group_size, void* hip_stream);
 
 /* Group absmax quantiser on the device, bit-identical to the benchmark quantiser the model files
  * use: per flat group of group_size values s = absmax / 127, q = round-half-away(w / s) clamped

@@ -35,10 +35,14 @@ SQ8_EPI_SWIGLU = 2
 DECODE_SYMBOLS = ("sq8_embedding", "sq8_rmsnorm", "sq8_add_rmsnorm", "sq8_rope_tables", "sq8_rope_kv",
                   "sq8_attention_decode", "sq8_swiglu", "sq8_add", "sq8_argmax_workspace_bytes",
                   "sq8_argmax", "sq8_quantize", "sq8_step_advance", "sq8_matmul_rmsnorm",
-                  "sq8_matmul_swiglu", "sq8_rope_attention_decode")
+                  "sq8_matmul_swiglu", "sq8_rope_attention_decode", "sq8_matmul_rmsnorm_swiglu",
+                  "sq8_argmax_advance")
 # include/sq8_batch.h
 BATCH_SYMBOLS = ("sq8_paged_rope_kv", "sq8_paged_attention", "sq8_paged_attention_ws",
                  "sq8_paged_attention_workspace_bytes", "sq8_swiglu_rows", "sq8_argmax_rows")
+
+# include/sq8_probe.h (measurement only)
+PROBE_SYMBOLS = ("sq8_probe_stream_read",)
 
 _lib = None
 
@@ -94,6 +98,8 @@ def lib() -> ctypes.CDLL:
             "sq8_step_advance": [vp, vp, vp, vp],
             "sq8_matmul_rmsnorm": [vp, vp, vp, vp, f32, vp, vp, vp, I, I, I, vp],
             "sq8_matmul_swiglu": [vp, vp, vp, vp, I, I, I, vp],
+            "sq8_matmul_rmsnorm_swiglu": [vp, vp, vp, vp, f32, vp, vp, vp, I, I, I, vp],
+            "sq8_argmax_advance": [vp, I, vp, sz, vp, vp, vp, I, I, vp, vp],
             "sq8_rope_attention_decode": [vp, I, I, I, vp, vp, vp, vp, vp, vp, I, vp],
             "sq8_paged_rope_kv": [vp, I, I, I, I, vp, vp, I, I, vp, vp, vp, vp, vp],
             "sq8_paged_attention": [vp, I, I, I, I, I, vp, vp, I, I, vp, vp, vp, vp],
@@ -101,6 +107,7 @@ def lib() -> ctypes.CDLL:
             "sq8_swiglu_rows": [vp, I, I, vp, vp],
             "sq8_argmax_rows": [vp, I, I, vp, vp],
             "sq8_matmul_noalloc": [vp, vp, vp, vp, I, I, I, I, vp],
+            "sq8_probe_stream_read": [vp, sz, vp, I, I, I, vp],
         }
         for name, args in sigs.items():
             fn = getattr(L, name)
@@ -328,6 +335,32 @@ def matmul_rmsnorm(x, res, x_out, norm_w, w, scales, y, group_size: int = 64, ep
     N, K = w.shape
     _call("sq8_matmul_rmsnorm", _ptr(x), _ptr(res), _ptr(x_out), _ptr(norm_w), eps, _ptr(w),
           _ptr(scales), _ptr(y), N, K, group_size, stream=stream)
+
+
+def probe_stream_read(buf, sink, workgroups_per_cu: int = 8, chunks_per_lane: int = 4,
+                      stream=None):
+    """Read-only streaming probe over buf (any dtype, 16-byte multiple); adds the wrapping uint32
+    sums of its 32-bit words into the counters of sink (an int32 device tensor)."""
+    _call("sq8_probe_stream_read", _ptr(buf), buf.numel() * buf.element_size(), _ptr(sink),
+          sink.numel(), workgroups_per_cu, chunks_per_lane, stream=stream)
+
+
+def matmul_rmsnorm_swiglu(x, res, x_out, norm_w, w, scales, y, group_size: int = 64,
+                          eps: float = 1e-6, stream=None):
+    """y = silu(g) * u with [g; u] = matmul(rmsnorm(x + res) * norm_w, w) (w = [w1; w3], y of
+    N/2 values); x + res also written to x_out (res, x_out may be None)."""
+    N, K = w.shape
+    _call("sq8_matmul_rmsnorm_swiglu", _ptr(x), _ptr(res), _ptr(x_out), _ptr(norm_w), eps,
+          _ptr(w), _ptr(scales), _ptr(y), N, K, group_size, stream=stream)
+
+
+def argmax_advance(logits, pos, token, emb_table, x, workspace: Workspace, stream=None):
+    """*token = first argmax of logits, *pos += 1, x = emb_table[*token] (one launch)."""
+    n = logits.numel()
+    vocab, dim = emb_table.shape
+    ws_ptr, ws_n = workspace.get(int(lib().sq8_argmax_workspace_bytes(n)))
+    _call("sq8_argmax_advance", _ptr(logits), n, ws_ptr, ws_n, _ptr(pos), _ptr(token),
+          _ptr(emb_table), vocab, dim, _ptr(x), stream=stream)
 
 
 def matmul_swiglu(gate_up, w, scales, y, group_size: int = 64, stream=None):

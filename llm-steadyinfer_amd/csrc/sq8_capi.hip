@@ -201,6 +201,22 @@ int sq8_matmul_rmsnorm(const float* x, const float* res, float* x_out, const flo
   return e == hipSuccess ? SQ8_OK : SQ8_ERR_LAUNCH;
 }
 
+int sq8_matmul_rmsnorm_swiglu(const float* x, const float* res, float* x_out,
+                              const float* norm_w, float eps, const int8_t* w,
+                              const float* scales, float* y, int N, int K, int group_size,
+                              void* hip_stream) {
+  const int v = validate_fused(x, w, scales, y, N, K, group_size);
+  if (v != SQ8_OK) return v;
+  if (!norm_w) return SQ8_ERR_NULL;
+  if (N % 2 != 0 || !aligned16(norm_w) || (res && !aligned16(res)) ||
+      (x_out && !aligned16(x_out)))
+    return SQ8_ERR_DIMS;
+  const hipError_t e = sq8::launch_gemv_norm_swiglu(x, res, x_out, norm_w, eps, w, scales, y, N,
+                                                    K, group_size,
+                                                    static_cast<hipStream_t>(hip_stream));
+  return e == hipSuccess ? SQ8_OK : SQ8_ERR_LAUNCH;
+}
+
 int sq8_matmul_swiglu(const float* gate_up, const int8_t* w, const float* scales, float* y, int N,
                       int K, int group_size, void* hip_stream) {
   const int v = validate_fused(gate_up, w, scales, y, N, K, group_size);

@@ -70,6 +70,9 @@ bool gemv_stream_fits(int M, int K);
 hipError_t launch_gemv_norm(const float* x, const float* res, float* x_out, const float* nw,
                             float eps, const int8_t* w, const float* s, float* y, int N, int K,
                             int gs, hipStream_t st);
+hipError_t launch_gemv_norm_swiglu(const float* x, const float* res, float* x_out,
+                                  const float* nw, float eps, const int8_t* w, const float* s,
+                                  float* y, int N, int K, int gs, hipStream_t st);
 hipError_t launch_gemv_swiglu(const float* ab, const int8_t* w, const float* s, float* y, int N,
                               int K, int gs, hipStream_t st);
 hipError_t launch_generic(const float* x, const int8_t* w, const float* s, float* y, int M, int N,

@@ -415,14 +415,26 @@ __device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) 
   return v > bv || (v == bv && i < bi);
 }
 
+// Optional decode-step tail run by the last workgroup once the winner is known: *pos += 1 and
+// the winner's embedding row is copied to x (the next step's input), so a captured step needs no
+// separate advance and embedding launches.
+struct Advance {
+  int32_t* pos;        // null: no advance
+  const float* emb;    // [vocab][dim]
+  int vocab, dim;
+  float* x;
+};
+
 __global__ __launch_bounds__(kBlock) void argmax_kernel(const float* __restrict__ logits, int n,
                                                         int32_t* __restrict__ out,
                                                         float* __restrict__ wval,
                                                         int* __restrict__ widx,
-                                                        unsigned* __restrict__ ticket) {
+                                                        unsigned* __restrict__ ticket,
+                                                        Advance adv) {
   __shared__ float sv[kBlockWaves];
   __shared__ int si[kBlockWaves];
   __shared__ bool last;
+  __shared__ int s_tok;
   const int base = blockIdx.x * kArgmaxChunk;
   float best = -INFINITY;
   int bi = INT_MAX;
@@ -488,9 +500,40 @@ __global__ __launch_bounds__(kBlock) void argmax_kernel(const float* __restrict_
           fi = ci;
         }
       }
-      out[0] = fi < n ? fi : 0;
+      s_tok = fi < n ? fi : 0;
+      out[0] = s_tok;
+      if (adv.pos) adv.pos[0] += 1;
       __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+  }
+  if (!adv.pos) return;  // uniform: a kernel argument
+  __syncthreads();
+  if (!last) return;     // uniform: published by the barrier
+  const int tok = s_tok;
+  if (tok < 0 || tok >= adv.vocab) return;
+  const float* row = adv.emb + static_cast<size_t>(tok) * adv.dim;
+  // Up to 4 float4 per thread per pass, all loads issued before the stores (a loop of dependent
+  // load-store pairs costs one memory round trip per element).
+  if (adv.dim % 4 == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(adv.x) & 15) == 0) {
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    float4* x4 = reinterpret_cast<float4*>(adv.x);
+    const int n4 = adv.dim / 4;
+    for (int i0 = 0; i0 < n4; i0 += 4 * kBlock) {
+      float4 v[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = i0 + j * kBlock + threadIdx.x;
+        v[j] = i < n4 ? r4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = i0 + j * kBlock + threadIdx.x;
+        if (i < n4) x4[i] = v[j];
+      }
+    }
+  } else {
+    for (int i = threadIdx.x; i < adv.dim; i += kBlock) adv.x[i] = row[i];
   }
 }
 
@@ -656,7 +699,22 @@ int sq8_argmax(const float* logits, int n, int32_t* out, void* workspace, size_t
   float* wval = reinterpret_cast<float*>(static_cast<char*>(workspace) + 256);
   int* widx = reinterpret_cast<int*>(wval + blocks);
   hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(kBlock), 0, stream_of(hip_stream), logits,
-                     n, out, wval, widx, ticket);
+                     n, out, wval, widx, ticket, Advance{});
+  return launched();
+}
+
+int sq8_argmax_advance(const float* logits, int n, void* workspace, size_t workspace_bytes,
+                       int32_t* pos, int32_t* token, const float* emb_table, int vocab, int dim,
+                       float* x, void* hip_stream) {
+  if (!logits || !pos || !token || !emb_table || !x) return SQ8_ERR_NULL;
+  if (n <= 0 || vocab <= 0 || dim <= 0) return SQ8_ERR_DIMS;
+  if (!workspace || workspace_bytes < sq8_argmax_workspace_bytes(n)) return SQ8_ERR_WORKSPACE;
+  const int blocks = (n + kArgmaxChunk - 1) / kArgmaxChunk;
+  unsigned* ticket = static_cast<unsigned*>(workspace);
+  float* wval = reinterpret_cast<float*>(static_cast<char*>(workspace) + 256);
+  int* widx = reinterpret_cast<int*>(wval + blocks);
+  hipLaunchKernelGGL(argmax_kernel, dim3(blocks), dim3(kBlock), 0, stream_of(hip_stream), logits,
+                     n, token, wval, widx, ticket, Advance{pos, emb_table, vocab, dim, x});
   return launched();
 }
 

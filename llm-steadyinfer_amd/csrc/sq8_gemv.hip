@@ -159,9 +159,13 @@ struct ProArgs {
 // lane reads the 4 float4 of its 16-element chunk, and without the swizzle lanes l and l+4 would
 // hit the same LDS banks in every ds_read_b128 (4-way conflicts). The caller's barrier publishes
 // the stage.
+// kProNorm stages r * nw (r = x + res) in the same single pass that sums r^2: the RMSNorm scale
+// rsqrt(mean(r^2) + eps) is a scalar of the row, so it multiplies the finished dot products
+// instead of every staged value, and the stage needs no reduction barrier of its own. The
+// per-wave sums of squares are left in the returned LDS array for norm_scale() after the barrier.
 template <int MT, int WV, int PRO>
-__device__ __forceinline__ void stage_x(const float* __restrict__ x, int M, int K,
-                                        const ProArgs& pro, float* xs) {
+__device__ __forceinline__ const float* stage_x(const float* __restrict__ x, int M, int K,
+                                                const ProArgs& pro, float* xs) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const float4* x4 = reinterpret_cast<const float4*>(x);
@@ -171,9 +175,12 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int M, int 
       const float4 v = i < M * K / 4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
       xs4[i ^ ((i >> 4) & 3)] = v;
     }
+    return nullptr;
   } else if (PRO == kProNorm) {
     __shared__ float red[WV];
     const float4* r4 = reinterpret_cast<const float4*>(pro.res);
+    const float4* n4 = reinterpret_cast<const float4*>(pro.nw);
+    float4* o4 = reinterpret_cast<float4*>(pro.x_out);
     float ss = 0.f;
     for (int i = tid; i < K / 4; i += WV * kWave) {
       float4 v = x4[i];
@@ -181,42 +188,50 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x, int M, int 
         const float4 r = r4[i];
         v = make_float4(v.x + r.x, v.y + r.y, v.z + r.z, v.w + r.w);
       }
+      if (o4 && blockIdx.x == 0) o4[i] = v;
       ss = fmaf(v.x, v.x, ss);
       ss = fmaf(v.y, v.y, ss);
       ss = fmaf(v.z, v.z, ss);
       ss = fmaf(v.w, v.w, ss);
+      const float4 g = n4[i];
+      xs4[i ^ ((i >> 4) & 3)] = make_float4(v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w);
     }
 #pragma unroll
     for (int off = 32; off >= 1; off /= 2) ss += __shfl_xor(ss, off, kWave);
     if (lane == 0) red[wave] = ss;
-    __syncthreads();
-    float total = red[0];
-#pragma unroll
-    for (int v = 1; v < WV; ++v) total += red[v];
-    const float scale = rsqrtf(total / static_cast<float>(K) + pro.eps);
-    const float4* n4 = reinterpret_cast<const float4*>(pro.nw);
-    float4* o4 = reinterpret_cast<float4*>(pro.x_out);
-    for (int i = tid; i < K / 4; i += WV * kWave) {
-      float4 v = x4[i];
-      if (r4) {
-        const float4 r = r4[i];
-        v = make_float4(v.x + r.x, v.y + r.y, v.z + r.z, v.w + r.w);
-      }
-      if (o4 && blockIdx.x == 0) o4[i] = v;
-      const float4 g = n4[i];
-      xs4[i ^ ((i >> 4) & 3)] = make_float4(scale * v.x * g.x, scale * v.y * g.y,
-                                            scale * v.z * g.z, scale * v.w * g.w);
-    }
+    return red;
   } else {
     for (int i = tid; i < K / 4; i += WV * kWave) {
       const float4 a = x4[i], g = x4[K / 4 + i];
       xs4[i ^ ((i >> 4) & 3)] = make_float4(silu_mul(a.x, g.x), silu_mul(a.y, g.y),
                                             silu_mul(a.z, g.z), silu_mul(a.w, g.w));
     }
+    return nullptr;
   }
 }
 
-template <int R, int U, int MT, int GS, bool TAIL, int WV = kWaves, int PRO = kProNone>
+// The RMSNorm scale of the staged row (after the barrier that published stage_x's sums): the
+// waves' sums of squares are added in wave order, so every workgroup gets the same value.
+template <int WV>
+__device__ __forceinline__ float norm_scale(const float* red, int K, float eps) {
+  float total = red[0];
+#pragma unroll
+  for (int v = 1; v < WV; ++v) total += red[v];
+  return rsqrtf(total / static_cast<float>(K) + eps);
+}
+
+// Rows of block b: R consecutive rows, or with PAIR (R = 2, a fused [gate; up] weight of N = 2F
+// rows) the gate row b and its up row b + F, so that one wave holds both dot products of a
+// SwiGLU output. Blocks past the last read row N - 1 (their results are dropped).
+template <int R, bool PAIR>
+__device__ __forceinline__ int block_row(int b, int r, int N) {
+  return PAIR ? min(b + r * (N / 2), N - 1) : min(b * R + r, N - 1);
+}
+
+// With PAIR (M = 1, R = 2) the kernel writes y[b] = silu(g) * u for the row pair of block b
+// (the SwiGLU of a fused [gate; up] projection, N/2 outputs) instead of the two rows.
+template <int R, int U, int MT, int GS, bool TAIL, int WV = kWaves, int PRO = kProNone,
+          bool PAIR = false>
 __global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restrict__ x,
                                                          const int8_t* __restrict__ w,
                                                          const float* __restrict__ s,
@@ -225,7 +240,8 @@ __global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restri
   extern __shared__ float xs[];
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar address math
-  const int nblk = (N + R - 1) / R;
+  static_assert(!PAIR || (R == 2 && MT == 1), "row pairs: two rows, one token");
+  const int nblk = PAIR ? N / 2 : (N + R - 1) / R;
   const int GW = gridDim.x * WV;
   const int gs = GS ? GS : gs_rt;
   const int gpr = K / gs;
@@ -240,7 +256,7 @@ __global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restri
       const int kc = !TAIL || k < K ? k : 0;
 #pragma unroll
       for (int r = 0; r < R; ++r)
-        sc[u][r] = s[static_cast<size_t>(min(b * R + r, N - 1)) * gpr + kc / gs];
+        sc[u][r] = s[static_cast<size_t>(block_row<R, PAIR>(b, r, N)) * gpr + kc / gs];
     }
   };
   auto load_w = [&](int b, int st, i32x4 (&q)[U][R]) __attribute__((always_inline)) {
@@ -251,7 +267,7 @@ __global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restri
       const int kc = ok ? k : 0;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const int n = min(b * R + r, N - 1);
+        const int n = block_row<R, PAIR>(b, r, N);
         const i32x4 v = __builtin_nontemporal_load(
             reinterpret_cast<const i32x4*>(w + static_cast<size_t>(n) * K + kc));
         q[u][r] = ok ? v : i32x4{0, 0, 0, 0};
@@ -273,9 +289,10 @@ __global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restri
     load_scales(b, 0, scn);
   }
 
-  stage_x<MT, WV, PRO>(x, M, K, pro, xs);
+  const float* red = stage_x<MT, WV, PRO>(x, M, K, pro, xs);
   __syncthreads();
   if constexpr (!kEarly) load_scales(b, 0, scn);
+  const float rs = PRO == kProNorm ? norm_scale<WV>(red, K, pro.eps) : 1.f;
 
   float acc[R * MT];
 #pragma unroll
@@ -307,10 +324,14 @@ __global__ __launch_bounds__(WV * kWave) void sweep_kernel(const float* __restri
     if (st == nsteps - 1) {
       wave_reduce_scatter<R * MT>(acc, lane);
       constexpr int kSpan = kWave / (R * MT);
-      if ((lane & (kSpan - 1)) == 0) {
+      if constexpr (PAIR) {
+        const float u = __shfl(acc[0], kSpan, kWave);  // the up row's sum (value index 1)
+        if (lane == 0 && b < nblk) y[b] = silu_mul(acc[0] * rs, u * rs);
+      } else if ((lane & (kSpan - 1)) == 0) {
         const int idx = lane / kSpan, r = idx / MT, t = idx % MT;
         const int n = b * R + r;
-        if (n < N && t < M) y[static_cast<size_t>(t) * N + n] = acc[0];
+        if (n < N && t < M) y[static_cast<size_t>(t) * N + n] = PRO == kProNorm ? acc[0] * rs
+                                                                               : acc[0];
       }
 #pragma unroll
       for (int i = 0; i < R * MT; ++i) acc[i] = 0.f;
@@ -366,9 +387,10 @@ __global__ __launch_bounds__(WV * kWave) void splitrow_kernel(const float* __res
   // staging); with a plain copy of x they follow it, as in sweep_kernel.
   constexpr bool kEarly = PRO != kProNone;
   if constexpr (kEarly) issue();
-  stage_x<1, WV, PRO>(x, 1, K, pro, xs);
+  const float* red = stage_x<1, WV, PRO>(x, 1, K, pro, xs);
   __syncthreads();
   if constexpr (!kEarly) issue();
+  const float rs = PRO == kProNorm ? norm_scale<WV>(red, K, pro.eps) : 1.f;
   float acc = 0.f;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -390,7 +412,7 @@ __global__ __launch_bounds__(WV * kWave) void splitrow_kernel(const float* __res
 #pragma unroll
     for (int i = 1; i < KS; ++i) v += part[tid * KS + i];
     const int n = blockIdx.x * RW + tid;
-    if (n < N) y[n] = v;
+    if (n < N) y[n] = PRO == kProNorm ? v * rs : v;
   }
 }
 
@@ -456,6 +478,16 @@ int cu_count() {
 
 namespace {
 
+#ifndef SQ8_GEMV_NARROW_WPC
+#define SQ8_GEMV_NARROW_WPC 16
+#endif
+#ifndef SQ8_GEMV_PAIR_WV
+#define SQ8_GEMV_PAIR_WV 8
+#endif
+#ifndef SQ8_GEMV_PAIR_WPC
+#define SQ8_GEMV_PAIR_WPC 16
+#endif
+
 // LDS bytes the stream kernel may use for staged token rows (MT * K fp32).
 constexpr size_t kStreamLdsMax = 64 * 1024;
 // Two token rows of long K (down projections) may stage up to 128 KiB: fewer workgroups per CU,
@@ -463,38 +495,40 @@ constexpr size_t kStreamLdsMax = 64 * 1024;
 constexpr size_t kStreamLdsTwoRows = 128 * 1024;
 
 // WV waves per workgroup; 16 waves per CU in total, fewer when there are fewer row blocks.
-template <int R, int U, int MT, int GS, int WV, int PRO>
+template <int R, int U, int MT, int GS, int WV, int PRO, bool PAIR>
 hipError_t launch_sweep_t(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
-                          int K, int gs, const ProArgs& pro, hipStream_t st) {
+                          int K, int gs, const ProArgs& pro, hipStream_t st, int wpc) {
   const size_t lds = static_cast<size_t>(MT) * K * sizeof(float);
   const int nblk = (N + R - 1) / R;
-  const int grid = min((nblk + WV - 1) / WV, (16 / WV) * cu_count());
+  const int grid = min((nblk + WV - 1) / WV, (wpc / WV) * cu_count());
   if (lds > 64 * 1024) {  // above 64 KiB the dynamic LDS size needs the opt-in attribute
     static std::atomic<uint64_t> done_full{0}, done_tail{0};
     hipError_t e = ensure_dynamic_lds(
-        reinterpret_cast<const void*>(sweep_kernel<R, U, MT, GS, false, WV, PRO>),
+        reinterpret_cast<const void*>(sweep_kernel<R, U, MT, GS, false, WV, PRO, PAIR>),
         kStreamLdsTwoRows, done_full);
     if (e == hipSuccess)
       e = ensure_dynamic_lds(
-          reinterpret_cast<const void*>(sweep_kernel<R, U, MT, GS, true, WV, PRO>),
+          reinterpret_cast<const void*>(sweep_kernel<R, U, MT, GS, true, WV, PRO, PAIR>),
           kStreamLdsTwoRows, done_tail);
     if (e != hipSuccess) return e;
   }
   if (K % (1024 * U) == 0) {
-    hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, false, WV, PRO>), dim3(grid), dim3(WV * kWave),
+    hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, false, WV, PRO, PAIR>), dim3(grid), dim3(WV * kWave),
                        lds, st, x, w, s, y, M, N, K, gs, pro);
   } else {
-    hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, true, WV, PRO>), dim3(grid), dim3(WV * kWave),
+    hipLaunchKernelGGL((sweep_kernel<R, U, MT, GS, true, WV, PRO, PAIR>), dim3(grid), dim3(WV * kWave),
                        lds, st, x, w, s, y, M, N, K, gs, pro);
   }
   return hipGetLastError();
 }
 
-template <int R, int U, int WV, int MT, int PRO = kProNone>
+// wpc: resident waves per CU the grid is sized for.
+template <int R, int U, int WV, int MT, int PRO = kProNone, bool PAIR = false>
 hipError_t launch_sweep(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
-                        int K, int gs, hipStream_t st, const ProArgs& pro = {}) {
-  return gs == 64 ? launch_sweep_t<R, U, MT, 64, WV, PRO>(x, w, s, y, M, N, K, gs, pro, st)
-                  : launch_sweep_t<R, U, MT, 0, WV, PRO>(x, w, s, y, M, N, K, gs, pro, st);
+                        int K, int gs, hipStream_t st, const ProArgs& pro = {}, int wpc = 16) {
+  return gs == 64
+             ? launch_sweep_t<R, U, MT, 64, WV, PRO, PAIR>(x, w, s, y, M, N, K, gs, pro, st, wpc)
+             : launch_sweep_t<R, U, MT, 0, WV, PRO, PAIR>(x, w, s, y, M, N, K, gs, pro, st, wpc);
 }
 
 // Configurations measured best on the Llama-3-8B and Qwen2-1.5B shapes. Rows of 8 KiB and more:
@@ -539,9 +573,10 @@ hipError_t launch_stream(const float* x, const int8_t* w, const float* s, float*
   }
   const int u = K <= 1024 ? 1 : (K <= 2048 ? 2 : 4);
   if (N <= 8192) {
-    if (u == 1) return launch_sweep<1, 1, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
-    if (u == 2) return launch_sweep<1, 2, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
-    return launch_sweep<1, 4, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
+    const int wpc = SQ8_GEMV_NARROW_WPC;
+    if (u == 1) return launch_sweep<1, 1, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro, wpc);
+    if (u == 2) return launch_sweep<1, 2, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro, wpc);
+    return launch_sweep<1, 4, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro, wpc);
   }
   if (u == 1) return launch_sweep<2, 1, 4, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
   if (u == 2) return launch_sweep<2, 2, 4, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
@@ -599,6 +634,21 @@ hipError_t launch_gemv_norm(const float* x, const float* res, float* x_out, cons
                             int gs, hipStream_t st) {
   const ProArgs pro{res, x_out, nw, eps};
   return launch_stream<1, kProNorm>(x, w, s, y, 1, N, K, gs, st, pro);
+}
+
+hipError_t launch_gemv_norm_swiglu(const float* x, const float* res, float* x_out,
+                                  const float* nw, float eps, const int8_t* w, const float* s,
+                                  float* y, int N, int K, int gs, hipStream_t st) {
+  // Row pairs (gate b, up b + N/2) in two-row blocks, 4-wave workgroups, steps of up to 4 KiB
+  // per row: the configuration of the plain wide-output GEMV with two rows per wave.
+  const ProArgs pro{res, x_out, nw, eps};
+  constexpr int WV = SQ8_GEMV_PAIR_WV;
+  const int wpc = SQ8_GEMV_PAIR_WPC;
+  if (K <= 1024)
+    return launch_sweep<2, 1, WV, 1, kProNorm, true>(x, w, s, y, 1, N, K, gs, st, pro, wpc);
+  if (K <= 2048)
+    return launch_sweep<2, 2, WV, 1, kProNorm, true>(x, w, s, y, 1, N, K, gs, st, pro, wpc);
+  return launch_sweep<2, 4, WV, 1, kProNorm, true>(x, w, s, y, 1, N, K, gs, st, pro, wpc);
 }
 
 hipError_t launch_gemv_swiglu(const float* ab, const int8_t* w, const float* s, float* y, int N,

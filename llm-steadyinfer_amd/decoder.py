@@ -10,10 +10,12 @@ torch supplies device memory, streams and graph capture only. One decode step is
 
 with the residual add of each block folded into the next RMSNorm. With ``fused=True`` (the
 default) every add + RMSNorm runs inside the prologue of the projection that consumes it
-(sq8_matmul_rmsnorm, the residual stream ping-ponging between two buffers), SwiGLU inside the
-down projection's (sq8_matmul_swiglu) and RoPE + cache write inside attention
-(sq8_rope_attention_decode): 5 launches per layer instead of 9. Positions and tokens
-live in device memory, so the step is captured once into a HIP graph and replayed per token.
+(sq8_matmul_rmsnorm, the residual stream ping-ponging between two buffers), SwiGLU in the
+gate/up projection's epilogue (sq8_matmul_rmsnorm_swiglu: one wave computes a gate row and its up
+row) and RoPE + cache write inside attention (sq8_rope_attention_decode): 5 launches per layer
+instead of 9; the step ends with one launch for argmax, position advance and the next token's
+embedding (sq8_argmax_advance). Positions and tokens live in device memory, so the step is
+captured once into a HIP graph and replayed per token.
 
 Weights come from an INT8 model file (model_file.py / the reference layout) or from an on-device
 random init of the same distribution (for benchmarks of the large shapes without writing a file).
@@ -25,9 +27,9 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import (Workspace, add_rmsnorm, argmax, attention_decode, embedding, lib, matmul,
-               matmul_rmsnorm, matmul_swiglu, quantize, rmsnorm, rope_attention_decode, rope_kv,
-               rope_tables, step_advance, swiglu)
+from . import (Workspace, add_rmsnorm, argmax, argmax_advance, attention_decode, embedding, lib,
+               matmul, matmul_rmsnorm, matmul_rmsnorm_swiglu, matmul_swiglu, quantize, rmsnorm,
+               rope_attention_decode, rope_kv, rope_tables, step_advance, swiglu)
 from .model_file import ModelConfig, ModelFile
 
 EPS = 1e-6
@@ -154,11 +156,14 @@ class Int8Decoder:
         matmul_rmsnorm(x, res, x_out, norm, q, s, y, self.gs, EPS, stream=stream)
 
     def _launch_step_fused(self, stream, want_logits: bool):
+        """A prompt step (want_logits False) embeds self.token itself; a decode step starts from
+        self.x, which the previous step's sq8_argmax_advance (or begin_decode) filled."""
         cfg = self.cfg
         L, d, kv = cfg.layer_num, cfg.dim, self.kv_dim
         w = self.w
         cur, other = self.x, self.x2
-        embedding(w["emb"], self.token, cur, stream=stream)
+        if not want_logits:
+            embedding(w["emb"], self.token, cur, stream=stream)
         for l in range(L):
             if l == 0:
                 self._mm_norm(cur, None, None, w["norm"][0], w["qkv"][0], self.qkv, stream)
@@ -169,16 +174,23 @@ class Int8Decoder:
                                   self.sin, self.cos, self.kcache[l], self.vcache[l], self.att,
                                   self.max_seq, stream=stream)
             self._mm(self.att, w["o"][l], self.proj, stream)
-            self._mm_norm(cur, self.proj, other, w["norm"][L + l], w["gu"][l], self.gu, stream)
+            q, s = w["gu"][l]
+            matmul_rmsnorm_swiglu(cur, self.proj, other, w["norm"][L + l], q, s, self.hid,
+                                  self.gs, EPS, stream=stream)
             cur, other = other, cur
-            q, s = w["down"][l]
-            matmul_swiglu(self.gu, q, s, self.proj, self.gs, stream=stream)
+            self._mm(self.hid, w["down"][l], self.proj, stream)
         if want_logits:
             self._mm_norm(cur, self.proj, None, w["norm"][2 * L], w["cls"], self.logits, stream)
-            argmax(self.logits, self.next, workspace=self.argmax_ws, stream=stream)
-            step_advance(self.pos, self.token, self.next, stream=stream)
+            argmax_advance(self.logits, self.pos, self.token, w["emb"], self.x, self.argmax_ws,
+                           stream=stream)
         else:
             step_advance(self.pos, self.token, self.token, stream=stream)
+
+    def begin_decode(self, stream=None):
+        """Embed self.token into the first step's input (the fused decode step does not embed:
+        sq8_argmax_advance leaves the next token's row in place)."""
+        if self.fused:
+            embedding(self.w["emb"], self.token, self.x, stream=stream)
 
     def _launch_step_plain(self, stream, want_logits: bool):
         """Enqueue one token: reads self.token / self.pos, writes self.next (when want_logits)
@@ -217,7 +229,8 @@ class Int8Decoder:
         self.vcache.zero_()
 
     def capture(self):
-        """Capture one logits-producing step into a HIP graph (replayed by generate)."""
+        """Capture one logits-producing step into a HIP graph (replayed by generate). Capturing
+        records the launches without running them, so the decoder's state is unchanged."""
         torch = self.torch
         s = torch.cuda.Stream(device=self.device)
         s.wait_stream(torch.cuda.current_stream())
@@ -240,6 +253,7 @@ class Int8Decoder:
         out = torch.empty(n_new, dtype=torch.int32, device=self.device)
         if use_graph and self.graph is None:
             self.capture()
+        self.begin_decode(stream)
         for i in range(n_new):
             if use_graph:
                 self.graph.replay()

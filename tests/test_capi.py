@@ -23,7 +23,7 @@ def declared_functions(headers=(HEADER,)):
 def test_header_declares_expected(sq8):
     assert declared_functions() == sorted(sq8.EXPORTED_SYMBOLS)
     assert declared_functions(HEADERS) == sorted(sq8.EXPORTED_SYMBOLS + sq8.DECODE_SYMBOLS +
-                                                 sq8.BATCH_SYMBOLS)
+                                                 sq8.BATCH_SYMBOLS + sq8.PROBE_SYMBOLS)
 
 
 def test_library_exports_every_declared_symbol(sq8):

@@ -30,6 +30,14 @@ def test_decode_ops_reject_bad_arguments(sq8):
     assert L.sq8_matmul_rmsnorm(FAKE, None, None, FAKE, 1e-6, FAKE, FAKE, FAKE, 8, 20000, 16, None) == sq8.SQ8_ERR_DIMS
     assert L.sq8_matmul_swiglu(FAKE, FAKE, FAKE, FAKE, 8, 96, 64, None) == sq8.SQ8_ERR_GROUP
     assert L.sq8_matmul_swiglu(FAKE + 4, FAKE, FAKE, FAKE, 8, 128, 64, None) == sq8.SQ8_ERR_DIMS
+    assert L.sq8_matmul_rmsnorm_swiglu(FAKE, None, None, FAKE, 1e-6, FAKE, FAKE, FAKE, 7, 64, 64,
+                                       None) == sq8.SQ8_ERR_DIMS   # odd N
+    assert L.sq8_matmul_rmsnorm_swiglu(FAKE, None, None, None, 1e-6, FAKE, FAKE, FAKE, 8, 64, 64,
+                                       None) == sq8.SQ8_ERR_NULL
+    assert L.sq8_argmax_advance(FAKE, 8, FAKE, 4096, None, FAKE, FAKE, 8, 8, FAKE,
+                                None) == sq8.SQ8_ERR_NULL
+    assert L.sq8_argmax_advance(FAKE, 8, FAKE, 0, FAKE, FAKE, FAKE, 8, 8, FAKE,
+                                None) == sq8.SQ8_ERR_WORKSPACE
 
 
 def _t(a, dev, dtype=None):
@@ -209,6 +217,55 @@ def test_matmul_rmsnorm_equals_separate_ops(sq8, dev, N, K, with_res):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("N,K,with_res", [(17920, 1536, True), (28672, 4096, True),
+                                          (28672, 4096, False), (96, 256, True), (8, 2048, True)])
+def test_matmul_rmsnorm_swiglu_equals_separate_ops(sq8, dev, N, K, with_res):
+    """Add + RMSNorm prologue, fused [w1; w3] GEMV and SwiGLU epilogue in one launch: against the
+    oracle's rmsnorm, float64 matmul and swiglu; the residual stream is written once."""
+    import torch
+    rng = np.random.default_rng(N + 3 * K)
+    x = (rng.standard_normal(K) * 2).astype(np.float32)
+    r = rng.standard_normal(K).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    _, q, s = o.make_case(1, N, K, 64, seed=N + K)
+    y = torch.full((N // 2,), float("nan"), device=dev)
+    xo = torch.full((K,), 9.0, device=dev)
+    sq8.matmul_rmsnorm_swiglu(_t(x, dev), _t(r, dev) if with_res else None, xo, _t(g, dev),
+                              _t(q, dev), _t(s, dev), y)
+    xin = (x + r) if with_res else x
+    xn = do.rmsnorm(xin, g).astype(np.float32)
+    gu = o.matmul_f64(xn.reshape(1, -1), q, s, 64).reshape(-1)
+    ref = do.swiglu(gu[:N // 2], gu[N // 2:])
+    elem, norm = o.rel_errors(y.cpu().numpy().reshape(1, -1), ref.reshape(1, -1))
+    print(f"fused norm+swiglu N={N} K={K}: elem {elem:.2e} norm {norm:.2e}")
+    assert elem <= 1e-3 and norm <= 1e-5
+    np.testing.assert_array_equal(xo.cpu().numpy(), xin)
+
+
+@pytest.mark.gpu
+def test_argmax_advance(sq8, dev):
+    """Argmax (first maximum), position advance and the winner's embedding row in one launch;
+    the workspace is reused (its ticket is left zero)."""
+    import torch
+    rng = np.random.default_rng(11)
+    vocab, dim = 5003, 96
+    emb = rng.standard_normal((vocab, dim)).astype(np.float32)
+    emb_t = _t(emb, dev)
+    ws = sq8.Workspace(dev)
+    pos = torch.tensor([17], dtype=torch.int32, device=dev)
+    tok = torch.tensor([3], dtype=torch.int32, device=dev)
+    x = torch.zeros(dim, device=dev)
+    for i, n in enumerate((vocab, vocab, 4096, 7)):
+        v = rng.standard_normal(n).astype(np.float32)
+        if i == 1:
+            v[[4000, 2500]] = 50.0            # tie: the first index wins
+        sq8.argmax_advance(_t(v, dev), pos, tok, emb_t, x, ws)
+        want = do.argmax_first(v)
+        assert int(tok.item()) == want and int(pos.item()) == 18 + i
+        np.testing.assert_array_equal(x.cpu().numpy(), emb[want])
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("N,K", [(1536, 8960), (1001, 10240), (2048, 8256), (4096, 14336), (64, 1024)])
 def test_matmul_swiglu_equals_separate_ops(sq8, dev, N, K):
     import torch
@@ -255,3 +312,20 @@ def test_rope_attention_equals_separate_ops(sq8, dev, heads, kv_heads, hs, pos):
     ref = do.attention(qr, kc2.cpu().numpy(), vc2.cpu().numpy(), pos, heads, kv_heads, hs)
     _close(out.cpu().numpy(), ref, 2e-6, "fused rope+attention")
     _close(out2.cpu().numpy(), ref, 2e-6, "separate")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("nbytes,wpc,u", [(16, 1, 1), (4096 * 16 + 48, 4, 4), (1 << 24, 8, 8),
+                                          (3 * (1 << 20) + 16, 2, 2)])
+def test_probe_stream_read_sums_every_word(sq8, dev, nbytes, wpc, u):
+    """The bandwidth probe reads every byte once: its wrapping uint32 word sum matches numpy."""
+    import torch
+    rng = np.random.default_rng(nbytes)
+    a = rng.integers(0, 2 ** 32, nbytes // 4, dtype=np.uint64).astype(np.uint32)
+    buf = torch.from_numpy(a.view(np.int32)).to(dev)
+    sink = torch.zeros(1000, dtype=torch.int32, device=dev)
+    sq8.probe_stream_read(buf, sink, wpc, u)
+    sq8.probe_stream_read(buf, sink, wpc, u)
+    want = (2 * int(a.astype(np.uint64).sum())) % (1 << 32)
+    got = int(sink.cpu().numpy().view(np.uint32).astype(np.uint64).sum()) % (1 << 32)
+    assert got == want

@@ -70,6 +70,7 @@ def test_logits_match_oracle_at_each_step(dev, tmp_path, fused):
     tok = 17
     for pos in range(12):
         D.token.fill_(tok)
+        D.begin_decode(stream)  # a decode step starts from the embedded token row
         D._launch_step(stream, want_logits=True)
         lg = D.logits.cpu().numpy()
         rl = ref.step(tok, pos)
