@@ -232,6 +232,34 @@ struct PTile {
   static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 };
 
+#ifndef SQ8_GEMM_GM
+#define SQ8_GEMM_GM 4
+#endif
+// Output tile (bx, by, bz) of the GEMM's hardware workgroup id. MI355X hands workgroups to its 8
+// XCDs round robin (workgroup b runs on XCD b % 8), and each XCD has its own L2. The grid is
+// renumbered so that each XCD works through one contiguous range of tiles, ordered in bands of
+// GM M-tiles (column by column within a band): the ~32 workgroups an XCD runs at once then
+// share GM activation tiles and 32 / GM weight tiles in its L2, where launch order spread every
+// N-tile over all 8 XCDs and each M-tile over several. A bijection when the grid is a multiple
+// of 8 workgroups; otherwise the launch order is kept.
+__device__ __forceinline__ void gemm_tile_coords(int& bx, int& by, int& bz) {
+  const int X = gridDim.x, Y = gridDim.y, Z = gridDim.z;
+  const int total = X * Y * Z;
+  const int b = blockIdx.x + X * (blockIdx.y + Y * blockIdx.z);
+  bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+  constexpr int GM = SQ8_GEMM_GM;
+  if (GM <= 0 || total % 8 != 0) return;
+  const int L = (b & 7) * (total >> 3) + (b >> 3);
+  const int XY = X * Y;
+  bz = L / XY;
+  const int r = L - bz * XY;
+  const int band = r / (GM * X), row0 = band * GM;
+  const int rows = min(GM, Y - row0);
+  const int q = r - band * GM * X;
+  by = row0 + q % rows;
+  bx = q / rows;
+}
+
 template <int WAVES_M, int WAVES_N, int TM, int TN, int STAGES, int GPS>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
     const _Float16* xh, const _Float16* xl, const float* __restrict__ rscale, const int8_t* w,
@@ -243,9 +271,11 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-  const int n0 = blockIdx.x * T::BN, m0 = blockIdx.y * T::BM;
+  int bx, by, bz;
+  gemm_tile_coords(bx, by, bz);
+  const int n0 = bx * T::BN, m0 = by * T::BM;
   const int nsteps = K / T::KB;  // stages of GPS groups; the split is in stages
-  const int st_begin = blockIdx.z * groups_per_split;
+  const int st_begin = bz * groups_per_split;
   const int st_end = min(nsteps, st_begin + groups_per_split);
   const int gpr = K / gs;
   // Weight row behind tile column c (0 <= c < BN). SwiGLU: the workgroup owns features
@@ -253,7 +283,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
   // features and tiles j + TN/2 their up rows (F rows further on), so one lane holds both halves
   // of each output.
   const bool swiglu = epi.mode == kEpiSwiglu;
-  const int F = N / 2, f0 = blockIdx.x * (T::BN / 2);
+  const int F = N / 2, f0 = bx * (T::BN / 2);
   auto feat = [&](int c) __attribute__((always_inline)) {  // SwiGLU feature of tile column c
     const int tl = c >> 5, jj = (tl % TN) % HT;
     return f0 + ((tl / TN) * HT + jj) * 32 + (c & 31);
@@ -457,7 +487,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
   wait_vmcnt<0>();
 
   if (gridDim.z > 1) {  // split-K partial tile: raw sums at the weight row's column
-    float* dst = out + static_cast<size_t>(blockIdx.z) * M * N;
+    float* dst = out + static_cast<size_t>(bz) * M * N;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
