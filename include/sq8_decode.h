@@ -70,6 +70,20 @@ int sq8_rope_attention_decode(const float* qkv, int head_num, int kv_head_num, i
                               float* key_cache, float* value_cache, float* out, int max_seq,
                               void* hip_stream);
 
+/* sq8_rope_attention_decode with the positions split over several workgroups per head (the
+ * flash-decoding split and combine of mha_kernel.cu:178-341, here in one launch: the last chunk
+ * of a head to finish merges the chunks). The split is fixed by max_seq (up to 16 chunks of a
+ * multiple of 64 positions); chunks past *pos exit at once, and a single live chunk writes its
+ * output directly. The workspace (sq8_decode_attention_workspace_bytes; 0: no split for this
+ * max_seq) must be zero before its first use and is left ready for the next call; calls that
+ * share a workspace must not overlap. workspace == NULL runs the unsplit kernel. */
+size_t sq8_decode_attention_workspace_bytes(int head_num, int head_size, int max_seq);
+int sq8_rope_attention_decode_ws(const float* qkv, int head_num, int kv_head_num, int head_size,
+                                 const int32_t* pos, const float* sin_cache,
+                                 const float* cos_cache, float* key_cache, float* value_cache,
+                                 float* out, int max_seq, void* workspace, size_t workspace_bytes,
+                                 void* hip_stream);
+
 /* out[i] = silu(a[i]) * b[i], silu(v) = v / (1 + exp(-v)) (swiglu_kernel_cu_fp32,
  * src/source/op/kernels/cuda/swiglu_kernel.cu:4-21). `out` may alias `a`. */
 int sq8_swiglu(const float* a, const float* b, float* out, int n, void* hip_stream);

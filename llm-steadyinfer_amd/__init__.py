@@ -36,7 +36,8 @@ DECODE_SYMBOLS = ("sq8_embedding", "sq8_rmsnorm", "sq8_add_rmsnorm", "sq8_rope_t
                   "sq8_attention_decode", "sq8_swiglu", "sq8_add", "sq8_argmax_workspace_bytes",
                   "sq8_argmax", "sq8_quantize", "sq8_step_advance", "sq8_matmul_rmsnorm",
                   "sq8_matmul_swiglu", "sq8_rope_attention_decode", "sq8_matmul_rmsnorm_swiglu",
-                  "sq8_argmax_advance")
+                  "sq8_argmax_advance", "sq8_decode_attention_workspace_bytes",
+                  "sq8_rope_attention_decode_ws")
 # include/sq8_batch.h
 BATCH_SYMBOLS = ("sq8_paged_rope_kv", "sq8_paged_attention", "sq8_paged_attention_ws",
                  "sq8_paged_attention_workspace_bytes", "sq8_swiglu_rows", "sq8_argmax_rows")
@@ -100,6 +101,7 @@ def lib() -> ctypes.CDLL:
             "sq8_matmul_swiglu": [vp, vp, vp, vp, I, I, I, vp],
             "sq8_matmul_rmsnorm_swiglu": [vp, vp, vp, vp, f32, vp, vp, vp, I, I, I, vp],
             "sq8_argmax_advance": [vp, I, vp, sz, vp, vp, vp, I, I, vp, vp],
+            "sq8_rope_attention_decode_ws": [vp, I, I, I, vp, vp, vp, vp, vp, vp, I, vp, sz, vp],
             "sq8_rope_attention_decode": [vp, I, I, I, vp, vp, vp, vp, vp, vp, I, vp],
             "sq8_paged_rope_kv": [vp, I, I, I, I, vp, vp, I, I, vp, vp, vp, vp, vp],
             "sq8_paged_attention": [vp, I, I, I, I, I, vp, vp, I, I, vp, vp, vp, vp],
@@ -113,6 +115,8 @@ def lib() -> ctypes.CDLL:
             fn = getattr(L, name)
             fn.argtypes = args
             fn.restype = I
+        L.sq8_decode_attention_workspace_bytes.argtypes = [I, I, I]
+        L.sq8_decode_attention_workspace_bytes.restype = sz
         L.sq8_noalloc_scratch_bytes.argtypes = []
         L.sq8_noalloc_scratch_bytes.restype = sz
         L.sq8_argmax_workspace_bytes.argtypes = [I]
@@ -371,11 +375,24 @@ def matmul_swiglu(gate_up, w, scales, y, group_size: int = 64, stream=None):
 
 
 def rope_attention_decode(qkv, head_num: int, kv_head_num: int, head_size: int, pos, sin_cache,
-                          cos_cache, kcache, vcache, out, max_seq: int, stream=None):
-    """RoPE on the token's q and k, cache write at *pos and attention, in one launch."""
-    _call("sq8_rope_attention_decode", _ptr(qkv), head_num, kv_head_num, head_size, _ptr(pos),
-          _ptr(sin_cache), _ptr(cos_cache), _ptr(kcache), _ptr(vcache), _ptr(out), max_seq,
-          stream=stream)
+                          cos_cache, kcache, vcache, out, max_seq: int, workspace=None,
+                          stream=None):
+    """RoPE on the token's q and k, cache write at *pos and attention, in one launch. With a
+    workspace (zero-filled before its first use, decode_attention_workspace_bytes() bytes) the
+    positions are split over several workgroups per head."""
+    if workspace is None:
+        _call("sq8_rope_attention_decode", _ptr(qkv), head_num, kv_head_num, head_size,
+              _ptr(pos), _ptr(sin_cache), _ptr(cos_cache), _ptr(kcache), _ptr(vcache), _ptr(out),
+              max_seq, stream=stream)
+    else:
+        _call("sq8_rope_attention_decode_ws", _ptr(qkv), head_num, kv_head_num, head_size,
+              _ptr(pos), _ptr(sin_cache), _ptr(cos_cache), _ptr(kcache), _ptr(vcache), _ptr(out),
+              max_seq, _ptr(workspace), workspace.numel() * workspace.element_size(),
+              stream=stream)
+
+
+def decode_attention_workspace_bytes(head_num: int, head_size: int, max_seq: int) -> int:
+    return int(lib().sq8_decode_attention_workspace_bytes(head_num, head_size, max_seq))
 
 
 # Thin wrappers over include/sq8_batch.h (continuous batching, paged KV cache).

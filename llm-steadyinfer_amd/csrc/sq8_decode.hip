@@ -4,6 +4,7 @@
 // at few launches and full-wave work: one workgroup per row for the norms, one per head for
 // attention, vectorised elementwise kernels. Reductions run in a fixed order (wave butterflies,
 // then waves in index order), so every result is deterministic.
+#include <algorithm>
 #include <float.h>
 #include <limits.h>
 #include <math.h>
@@ -200,18 +201,7 @@ __global__ void rope_kv_kernel(float* __restrict__ qkv, int dim, int kv_dim, int
   }
 }
 
-// One workgroup per query head.
-//  * ROPE (fused RoPE + cache write): q and the kv head's k are rotated here from the projection
-//    output qkv = [q | k | v]; the first query head of each kv group writes k and v to cache row
-//    pos, and every head uses its own rotated copies for position pos (so no workgroup reads a
-//    row another one is writing). Without ROPE, q is read as given and row pos from the cache.
-//  * Scores: thread t owns cache position t (t, t + 1024, ...) and reads its key row as float4
-//    loads that are all independent (one memory round trip per 1024 positions); q is broadcast
-//    from LDS.
-//  * Softmax over the scores in LDS: workgroup max and sum (fixed order).
-//  * Values: wave w of 16 takes positions w, w + 16, ... and lane l the dims l, l + 64, ...;
-//    eight positions per iteration keep eight independent loads in flight; the 16 waves' partial
-//    sums meet in LDS in wave order.
+// Arguments of the fused RoPE + cache write (ROPE variant of attention_decode_kernel).
 struct RopeArgs {
   int dim, kv_dim;
   const float* sin_cache;
@@ -222,6 +212,19 @@ struct RopeArgs {
 
 constexpr int kAttnBlock = 1024;
 constexpr int kAttnWaves = kAttnBlock / kWave;
+
+// Split of the positions over gridDim.y workgroups per head (flash-decoding, mha_kernel.cu:
+// 178-341, here with the combine in the same launch). chunk == 0: one workgroup per head.
+struct SplitArgs {
+  int chunk;          // positions per workgroup
+  int stride;         // floats per partial: head_size + 2 (outputs, max, sum)
+  float* part;        // [head_num][gridDim.y][stride]
+  unsigned* tickets;  // [head_num]: zero before the first call, left zero by every call
+};
+// Positions per split workgroup: 16 waves x 4 positions, one load round per wave.
+constexpr int kAttnSplitChunk = kAttnWaves * 4;
+constexpr int kAttnSplitMax = 16;  // workgroups per head at most
+constexpr int kAttnSplitMinSeq = 512;
 
 // One workgroup (16 waves) per query head, in a single memory round trip:
 //  * wave w owns the cache positions w, w + 16, w + 32, ...; lane l holds head dims l, l + 64,
@@ -234,40 +237,56 @@ constexpr int kAttnWaves = kAttnBlock / kWave;
 //  * with ROPE the workgroup first rotates q and the token's k (pairs (i, i + hs/2) at table
 //    column 2i), the group's leader writes k and v to cache row pos, and the token's own position
 //    is scored from LDS (the cache rows read are 0 .. pos-1, written by earlier steps).
+//  * with a split (sp.chunk > 0) workgroup (head, c) covers positions c*chunk .. +chunk-1 of the
+//    pos + 1 live ones (workgroups past the last live chunk exit at once). Each stores its
+//    un-normalised outputs, max and sum (agent-scope stores, acknowledged before the ticket),
+//    takes a ticket per head, and the last of the head's live chunks merges them in chunk order
+//    and resets the ticket. A single live chunk writes its output directly.
 template <int HS_MAX, bool ROPE>
 __global__ __launch_bounds__(kAttnBlock) void attention_decode_kernel(
     const float* __restrict__ q, const float* kcache, const float* vcache,
     const int32_t* __restrict__ pos_ptr, float* __restrict__ out, int head_num, int kv_head_num,
-    int head_size, RopeArgs ra) {
+    int head_size, RopeArgs ra, SplitArgs sp) {
   constexpr int DPL = HS_MAX / kWave;  // head dims per lane
-  constexpr int PCH = 4;               // cache positions per wave per chunk
+  // Cache positions per wave per chunk (two chunks in flight). 8 measured slower at every
+  // length on MI355X (32 heads of 128: 8.1 against 6.5 us at 32 positions).
+  constexpr int PCH = 4;
   constexpr int W = kAttnWaves;
   __shared__ __attribute__((aligned(16))) float s_q[HS_MAX];
   __shared__ float s_k[HS_MAX];
   __shared__ float s_v[HS_MAX];
   __shared__ float s_m[W], s_l[W];
   __shared__ float s_acc[W][HS_MAX];
+  __shared__ bool s_last;
   const int head = xcd_grouped_id(head_num / kv_head_num);
   const int pos = *pos_ptr;
   const int seq = pos + 1;
+  const int c = blockIdx.y;
+  // Short rows are not split: the merge's extra round trip costs more than the split saves
+  // below kAttnSplitMinSeq positions (MI355X, 32 heads of 128: 9.4 against 6.8 us at 64).
+  const int chunk = sp.chunk > 0 && seq > kAttnSplitMinSeq ? sp.chunk : seq;
+  const int nlive = (seq + chunk - 1) / chunk;
+  if (c >= nlive) return;  // uniform: no positions left for this chunk
+  const int p0 = c * chunk, p1 = min(seq, p0 + chunk);
   const int kv_dim = kv_head_num * head_size;
   const int group = head * kv_head_num / head_num;
   const int hoff = group * head_size;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // Positions read from the cache: all of them, or all but pos when pos comes from registers.
-  const int ncache = ROPE ? pos : seq;
+  // Positions read from the cache: the chunk's, without pos when pos comes from registers.
+  const int cend = min(p1, ROPE ? pos : seq);
+  const int ncache = max(cend - p0, 0);
   const int nmine = wave < ncache ? (ncache - 1 - wave) / W + 1 : 0;
   const int nch = (nmine + PCH - 1) / PCH;
 
   // Chunk c of this wave's rows into register buffer b. Branch-free: positions past the wave's
   // last (and dims past head_size) re-read a valid element and are never used.
   float kr[2][PCH][DPL], vr[2][PCH][DPL];
-  const int tmax = max(ncache - 1, 0);
-  auto load = [&](int b, int c) __attribute__((always_inline)) {
+  const int tmax = max(cend - 1, 0);
+  auto load = [&](int b, int ci) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < PCH; ++i) {
-      const int t = min(wave + (c * PCH + i) * W, tmax);
+      const int t = min(p0 + wave + (ci * PCH + i) * W, tmax);
       const float* krow = kcache + static_cast<size_t>(t) * kv_dim + hoff;
       const float* vrow = vcache + static_cast<size_t>(t) * kv_dim + hoff;
 #pragma unroll
@@ -282,7 +301,7 @@ __global__ __launch_bounds__(kAttnBlock) void attention_decode_kernel(
 
   if (ROPE) {
     const int half = head_size / 2;
-    const bool leader = head == (group * head_num + kv_head_num - 1) / kv_head_num;
+    const bool leader = c == 0 && head == (group * head_num + kv_head_num - 1) / kv_head_num;
     for (int i = threadIdx.x; i < half; i += kAttnBlock) {
       const float fci = ra.sin_cache[static_cast<size_t>(pos) * head_size + 2 * i];
       const float fcr = ra.cos_cache[static_cast<size_t>(pos) * head_size + 2 * i];
@@ -328,7 +347,7 @@ __global__ __launch_bounds__(kAttnBlock) void attention_decode_kernel(
     for (int j = 0; j < DPL; ++j) acc[j] = fmaf(acc[j], f, p * v[j]);
     m = mn;
   };
-  auto chunk = [&](int b, int c) __attribute__((always_inline)) {
+  auto consume_chunk = [&](int b, int ci) __attribute__((always_inline)) {
     float part[PCH];
 #pragma unroll
     for (int i = 0; i < PCH; ++i) {
@@ -343,17 +362,17 @@ __global__ __launch_bounds__(kAttnBlock) void attention_decode_kernel(
       for (int i = 0; i < PCH; ++i) part[i] += __shfl_xor(part[i], off, kWave);
 #pragma unroll
     for (int i = 0; i < PCH; ++i)
-      if (c * PCH + i < nmine) consume(part[i] * scale, vr[b][i]);
+      if (ci * PCH + i < nmine) consume(part[i] * scale, vr[b][i]);
   };
   // Register double buffer over chunks, the prefetch issued unconditionally (clamped index).
-  for (int c = 0; c < nch; c += 2) {
-    load(1, min(c + 1, nch - 1));
-    chunk(0, c);
-    if (c + 1 >= nch) break;
-    load(0, min(c + 2, nch - 1));
-    chunk(1, c + 1);
+  for (int ci = 0; ci < nch; ci += 2) {
+    load(1, min(ci + 1, nch - 1));
+    consume_chunk(0, ci);
+    if (ci + 1 >= nch) break;
+    load(0, min(ci + 2, nch - 1));
+    consume_chunk(1, ci + 1);
   }
-  if (ROPE && wave == pos % W) {  // the token's own position, from LDS
+  if (ROPE && pos < p1 && wave == (pos - p0) % W) {  // the token's own position, from LDS
     float a = 0.f, v[DPL];
 #pragma unroll
     for (int j = 0; j < DPL; ++j) {
@@ -377,16 +396,62 @@ __global__ __launch_bounds__(kAttnBlock) void attention_decode_kernel(
   float mx = s_m[0];
 #pragma unroll
   for (int w = 1; w < W; ++w) mx = fmaxf(mx, s_m[w]);
-  for (int d = threadIdx.x; d < head_size; d += kAttnBlock) {
+  if (nlive == 1) {
+    for (int d = threadIdx.x; d < head_size; d += kAttnBlock) {
+      float o = 0.f, lt = 0.f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float f = s_m[w] == -INFINITY ? 0.f : expf(s_m[w] - mx);
+        o = fmaf(s_acc[w][d], f, o);
+        lt = fmaf(s_l[w], f, lt);
+      }
+      out[head * head_size + d] = o / lt;
+    }
+    return;
+  }
+  // Split: this chunk's un-normalised outputs, max and sum.
+  float* pp = sp.part + (static_cast<size_t>(head) * gridDim.y + c) * sp.stride;
+  for (int d = threadIdx.x; d < head_size + 1; d += kAttnBlock) {
     float o = 0.f, lt = 0.f;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
       const float f = s_m[w] == -INFINITY ? 0.f : expf(s_m[w] - mx);
-      o = fmaf(s_acc[w][d], f, o);
+      if (d < head_size) o = fmaf(s_acc[w][d], f, o);
       lt = fmaf(s_l[w], f, lt);
+    }
+    if (d < head_size) {
+      __hip_atomic_store(pp + d, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      __hip_atomic_store(pp + head_size, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(pp + head_size + 1, lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(sp.tickets + head, 1u, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT) == static_cast<unsigned>(nlive - 1);
+  __syncthreads();
+  if (!s_last) return;
+  const float* hp = sp.part + static_cast<size_t>(head) * gridDim.y * sp.stride;
+  float gm = -INFINITY;
+  for (int ci = 0; ci < nlive; ++ci)
+    gm = fmaxf(gm, __hip_atomic_load(hp + ci * sp.stride + head_size, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT));
+  for (int d = threadIdx.x; d < head_size; d += kAttnBlock) {
+    float o = 0.f, lt = 0.f;
+    for (int ci = 0; ci < nlive; ++ci) {
+      const float* cp = hp + ci * sp.stride;
+      const float f = expf(__hip_atomic_load(cp + head_size, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT) - gm);
+      o = fmaf(__hip_atomic_load(cp + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), f, o);
+      lt = fmaf(__hip_atomic_load(cp + head_size + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                f, lt);
     }
     out[head * head_size + d] = o / lt;
   }
+  if (threadIdx.x == 0)
+    __hip_atomic_store(sp.tickets + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ void swiglu_kernel(const float* __restrict__ a, const float* __restrict__ b,
@@ -636,11 +701,11 @@ int sq8_attention_decode(const float* q, const float* key_cache, const float* va
   if (head_size <= 128)
     hipLaunchKernelGGL((attention_decode_kernel<128, false>), dim3(head_num), dim3(kAttnBlock), 0,
                        stream_of(hip_stream), q, key_cache, value_cache, pos, out, head_num,
-                       kv_head_num, head_size, RopeArgs{});
+                       kv_head_num, head_size, RopeArgs{}, SplitArgs{});
   else
     hipLaunchKernelGGL((attention_decode_kernel<256, false>), dim3(head_num), dim3(kAttnBlock), 0,
                        stream_of(hip_stream), q, key_cache, value_cache, pos, out, head_num,
-                       kv_head_num, head_size, RopeArgs{});
+                       kv_head_num, head_size, RopeArgs{}, SplitArgs{});
   return launched();
 }
 
@@ -648,22 +713,62 @@ int sq8_rope_attention_decode(const float* qkv, int head_num, int kv_head_num, i
                               const int32_t* pos, const float* sin_cache, const float* cos_cache,
                               float* key_cache, float* value_cache, float* out, int max_seq,
                               void* hip_stream) {
+  return sq8_rope_attention_decode_ws(qkv, head_num, kv_head_num, head_size, pos, sin_cache,
+                                      cos_cache, key_cache, value_cache, out, max_seq, nullptr, 0,
+                                      hip_stream);
+}
+
+// Workgroups per head of the split decode attention for a cache of max_seq rows, and the
+// positions each covers (a multiple of kAttnSplitChunk).
+static void decode_split(int max_seq, int& chunks, int& chunk) {
+  chunks = std::min((max_seq + kAttnSplitChunk - 1) / kAttnSplitChunk, kAttnSplitMax);
+  const int per = (max_seq + chunks - 1) / chunks;
+  chunk = (per + kAttnSplitChunk - 1) / kAttnSplitChunk * kAttnSplitChunk;
+}
+
+size_t sq8_decode_attention_workspace_bytes(int head_num, int head_size, int max_seq) {
+  if (head_num <= 0 || head_size <= 0 || head_size > 256 || max_seq <= 0) return 0;
+  int chunks, chunk;
+  decode_split(max_seq, chunks, chunk);
+  if (chunks < 2) return 0;
+  const size_t tickets = (static_cast<size_t>(head_num) * 4 + 255) / 256 * 256;
+  return tickets + static_cast<size_t>(head_num) * chunks * (head_size + 2) * sizeof(float);
+}
+
+int sq8_rope_attention_decode_ws(const float* qkv, int head_num, int kv_head_num, int head_size,
+                                 const int32_t* pos, const float* sin_cache,
+                                 const float* cos_cache, float* key_cache, float* value_cache,
+                                 float* out, int max_seq, void* workspace, size_t workspace_bytes,
+                                 void* hip_stream) {
   if (!qkv || !pos || !sin_cache || !cos_cache || !key_cache || !value_cache || !out)
     return SQ8_ERR_NULL;
   if (head_num <= 0 || kv_head_num <= 0 || head_num % kv_head_num || head_size <= 0 ||
       head_size % 2 || head_size > 256 || max_seq <= 0)
     return SQ8_ERR_DIMS;
   if (max_seq > (1 << 24)) return SQ8_ERR_DIMS;
+  const size_t need = sq8_decode_attention_workspace_bytes(head_num, head_size, max_seq);
+  if (workspace && workspace_bytes < need) return SQ8_ERR_WORKSPACE;
   const RopeArgs ra{head_num * head_size, kv_head_num * head_size, sin_cache, cos_cache, key_cache,
                     value_cache};
+  SplitArgs sp{};
+  int chunks = 1;
+  if (workspace && need > 0) {
+    int chunk;
+    decode_split(max_seq, chunks, chunk);
+    const size_t tickets = (static_cast<size_t>(head_num) * 4 + 255) / 256 * 256;
+    sp = SplitArgs{chunk, head_size + 2,
+                   reinterpret_cast<float*>(static_cast<char*>(workspace) + tickets),
+                   static_cast<unsigned*>(workspace)};
+  }
+  const dim3 grid(head_num, chunks);
   if (head_size <= 128)
-    hipLaunchKernelGGL((attention_decode_kernel<128, true>), dim3(head_num), dim3(kAttnBlock), 0,
+    hipLaunchKernelGGL((attention_decode_kernel<128, true>), grid, dim3(kAttnBlock), 0,
                        stream_of(hip_stream), qkv, key_cache, value_cache, pos, out, head_num,
-                       kv_head_num, head_size, ra);
+                       kv_head_num, head_size, ra, sp);
   else
-    hipLaunchKernelGGL((attention_decode_kernel<256, true>), dim3(head_num), dim3(kAttnBlock), 0,
+    hipLaunchKernelGGL((attention_decode_kernel<256, true>), grid, dim3(kAttnBlock), 0,
                        stream_of(hip_stream), qkv, key_cache, value_cache, pos, out, head_num,
-                       kv_head_num, head_size, ra);
+                       kv_head_num, head_size, ra, sp);
   return launched();
 }
 

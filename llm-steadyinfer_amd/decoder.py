@@ -27,7 +27,8 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import (Workspace, add_rmsnorm, argmax, argmax_advance, attention_decode, embedding, lib,
+from . import (Workspace, add_rmsnorm, argmax, argmax_advance, attention_decode,
+               decode_attention_workspace_bytes, embedding, lib,
                matmul, matmul_rmsnorm, matmul_rmsnorm_swiglu, matmul_swiglu, quantize, rmsnorm,
                rope_attention_decode, rope_kv, rope_tables, step_advance, swiglu)
 from .model_file import ModelConfig, ModelFile
@@ -68,6 +69,9 @@ class Int8Decoder:
         self.ws = Workspace(device)
         self.argmax_ws = Workspace(device)  # sized now: nothing is allocated during capture
         self.argmax_ws.get(int(lib().sq8_argmax_workspace_bytes(cfg.vocab)))
+        # Split-position attention: zero-filled once, every call leaves its tickets zero.
+        att = decode_attention_workspace_bytes(cfg.head_num, self.hs, max_seq)
+        self.att_ws = torch.zeros((att + 3) // 4, **i32) if att > 0 else None
         self.graph = None
 
     # ------------------------------------------------------------------ construction
@@ -172,7 +176,7 @@ class Int8Decoder:
                 cur, other = other, cur
             rope_attention_decode(self.qkv, cfg.head_num, cfg.kv_head_num, self.hs, self.pos,
                                   self.sin, self.cos, self.kcache[l], self.vcache[l], self.att,
-                                  self.max_seq, stream=stream)
+                                  self.max_seq, workspace=self.att_ws, stream=stream)
             self._mm(self.att, w["o"][l], self.proj, stream)
             q, s = w["gu"][l]
             matmul_rmsnorm_swiglu(cur, self.proj, other, w["norm"][L + l], q, s, self.hid,

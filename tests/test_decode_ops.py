@@ -38,6 +38,14 @@ def test_decode_ops_reject_bad_arguments(sq8):
                                 None) == sq8.SQ8_ERR_NULL
     assert L.sq8_argmax_advance(FAKE, 8, FAKE, 0, FAKE, FAKE, FAKE, 8, 8, FAKE,
                                 None) == sq8.SQ8_ERR_WORKSPACE
+    assert L.sq8_rope_attention_decode_ws(FAKE, 32, 8, 128, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE,
+                                          4096, FAKE, 16, None) == sq8.SQ8_ERR_WORKSPACE
+    # the split: up to 16 chunks of a multiple of 64 positions, tickets then partials
+    f = sq8.decode_attention_workspace_bytes
+    assert f(32, 128, 64) == 0                      # one chunk: no split
+    assert f(32, 128, 192) == 256 + 32 * 3 * 130 * 4
+    assert f(32, 128, 8192) == 256 + 32 * 16 * 130 * 4
+    assert f(100, 64, 1000) == 512 + 100 * 16 * 66 * 4
 
 
 def _t(a, dev, dtype=None):
@@ -312,6 +320,45 @@ def test_rope_attention_equals_separate_ops(sq8, dev, heads, kv_heads, hs, pos):
     ref = do.attention(qr, kc2.cpu().numpy(), vc2.cpu().numpy(), pos, heads, kv_heads, hs)
     _close(out.cpu().numpy(), ref, 2e-6, "fused rope+attention")
     _close(out2.cpu().numpy(), ref, 2e-6, "separate")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("heads,kv_heads,hs,max_seq", [(32, 8, 128, 192), (12, 2, 128, 4096),
+                                                       (4, 4, 64, 1000), (14, 2, 256, 300)])
+def test_split_rope_attention_matches_oracle(sq8, dev, heads, kv_heads, hs, max_seq):
+    """Positions split over up to 16 workgroups per head (rows past 512 positions), merged by the
+    last to finish: the cache row written and the output equal the unsplit launch's (cache
+    bitwise, output to the oracle's bound) at positions on and around chunk edges and the split
+    threshold, all calls on one workspace (its tickets are zero after each)."""
+    import torch
+    dim, kv = heads * hs, kv_heads * hs
+    nbytes = sq8.decode_attention_workspace_bytes(heads, hs, max_seq)
+    assert nbytes > 0
+    ws = torch.zeros((nbytes + 3) // 4, dtype=torch.int32, device=dev)
+    sin = torch.empty((max_seq, hs), device=dev)
+    cos = torch.empty((max_seq, hs), device=dev)
+    sq8.rope_tables(sin, cos, hs, max_seq, 1e6)
+    s_np, c_np = sin.cpu().numpy().astype(np.float64), cos.cpu().numpy().astype(np.float64)
+    rng = np.random.default_rng(heads + max_seq)
+    kc0 = rng.standard_normal((max_seq, kv)).astype(np.float32)
+    vc0 = rng.standard_normal((max_seq, kv)).astype(np.float32)
+    edges = {0, 1, 63, 64, 65, 127, 128, 511, 512, 513, 576, 640, 767, 768, 769}
+    for pos in sorted({p for p in edges if p < max_seq} | {max_seq // 2, max_seq - 2, max_seq - 1}):
+        qkv = rng.standard_normal(dim + 2 * kv).astype(np.float32)
+        p = _t(np.array([pos], np.int32), dev)
+        kc, vc, out = _t(kc0, dev), _t(vc0, dev), torch.full((dim,), float("nan"), device=dev)
+        sq8.rope_attention_decode(_t(qkv, dev), heads, kv_heads, hs, p, sin, cos, kc, vc, out,
+                                  max_seq, workspace=ws)
+        kc2, vc2, out2 = _t(kc0, dev), _t(vc0, dev), torch.empty(dim, device=dev)
+        sq8.rope_attention_decode(_t(qkv, dev), heads, kv_heads, hs, p, sin, cos, kc2, vc2, out2,
+                                  max_seq)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(kc.cpu().numpy(), kc2.cpu().numpy())
+        np.testing.assert_array_equal(vc.cpu().numpy(), vc2.cpu().numpy())
+        qr = do.rope(qkv[:dim], heads, hs, pos, s_np, c_np)
+        ref = do.attention(qr, kc2.cpu().numpy(), vc2.cpu().numpy(), pos, heads, kv_heads, hs)
+        _close(out.cpu().numpy(), ref, 2e-6, f"split rope+attention pos {pos}")
+        assert int(ws[:heads].abs().sum()) == 0
 
 
 @pytest.mark.gpu
