@@ -109,7 +109,8 @@ class Call:
 
 def cpu_baseline(torch, weights, budget_s=10.0):
     """Oracle CPU loop (reference CPU GEMM structure, OpenMP) on one layer's four projections at
-    M=1, repeated for about budget_s seconds; returns GB/s by the same byte formula."""
+    M=1: one rep = the four calls; reps repeated for about budget_s seconds (at least 10). Returns
+    the median rep's GB/s by the same byte formula, with the spread."""
     sys.path.insert(0, str(REPO))
     import numpy as np
     from oracle import sq8_oracle as o
@@ -118,19 +119,20 @@ def cpu_baseline(torch, weights, budget_s=10.0):
     xs = {p: rng.standard_normal((1, PROJ[p][1]), dtype=np.float32) for p in PROJ}
     for p, q, s in layer:  # warm-up
         o.matmul_cpu_loop(xs[p], q, s, GS)
-    total_b, reps, t0 = 0, 0, time.perf_counter()
-    while True:
+    rep_bytes = sum(algo_bytes(1, *PROJ[p]) for p in PROJ)
+    times, t0 = [], time.perf_counter()
+    while len(times) < 10 or time.perf_counter() - t0 < budget_s:
+        a = time.perf_counter()
         for p, q, s in layer:
             o.matmul_cpu_loop(xs[p], q, s, GS)
-            total_b += algo_bytes(1, *PROJ[p])
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    return {"value": round(total_b / el / 1e9, 2), "unit": "GB/s", "cores": o.max_threads(),
-            "kind": "port",
-            "sample": f"oracle sq8o_matmul_cpu_loop, M=1, one Llama-3-8B layer (qkv,o,gate_up,down), "
-                      f"{reps} reps in {el:.1f} s"}
+        times.append(time.perf_counter() - a)
+    rates = sorted(rep_bytes / t / 1e9 for t in times)
+    med = float(np.median(rates))
+    return {"value": round(med, 2), "unit": "GB/s", "cores": o.max_threads(), "kind": "port",
+            "statistic": f"median of {len(times)} reps (min {rates[0]:.1f}, max {rates[-1]:.1f})",
+            "sample": "oracle sq8o_matmul_cpu_loop (reference CPU GEMM loop, OpenMP), M=1, one "
+                      "rep = one Llama-3-8B layer's qkv, o, gate_up and down projections, "
+                      f"{time.perf_counter() - t0:.1f} s"}
 
 
 def decode_run(torch, n_prompt: int = 64, n_new: int = 128, seed: int = 0):
@@ -360,6 +362,8 @@ def main():
     ap.add_argument("--profile-decode-gemm", action="store_true",
                     help="short run for counter collection: the four projections at M = 8, 32 "
                          "and 64 (configs 2), 3 launches each on distinct layers")
+    ap.add_argument("--no-ceiling", action="store_true",
+                    help="skip the read-probe and copy ceilings at the projections' sizes")
     ap.add_argument("--no-llama-decode", action="store_true",
                     help="skip the Llama-3-8B batch-1 end-to-end decode")
     ap.add_argument("--profile-prefill", action="store_true",
@@ -543,28 +547,29 @@ def main():
     # rows of the sweep: 32 back-to-back launches of the shape).
     shape_bytes = [(p, algo_bytes(1, N, K)) for p, (N, K) in PROJ.items()] + \
         [("lm_head", algo_bytes(1, VOCAB, HIDDEN))]
-    rceil = read_ceiling(torch, sq8, dev, shape_bytes)
-    cceil = copy_ceiling(torch, dev, shape_bytes)
-    gemv_us = {r["proj"]: r["us"] for r in sweep if r["M"] == 1}
-    counts = {p: LAYERS for p in PROJ}
-    counts["lm_head"] = 1
-    per_shape = {}
-    for p, nb in shape_bytes:
-        rec = {"algo_bytes": nb, "read_probe_us": rceil[p]["us"], "copy_us": cceil[p]["us"],
-               "read_probe_setting": [rceil[p]["workgroups_per_cu"],
-                                      rceil[p]["chunks_per_lane"]]}
-        if p in gemv_us:
-            rec["gemv_us"] = gemv_us[p]
-            rec["gemv_GBps"] = round(nb / gemv_us[p] / 1e3, 1)
-            rec["gemv_frac_of_peak"] = round(nb / gemv_us[p] / 1e3 / HBM_PEAK_GBS, 4)
-            rec["gemv_frac_of_read_probe"] = round(rceil[p]["us"] / gemv_us[p], 3)
-        per_shape[p] = rec
-    ceil_step_us = sum(rceil[p]["us"] * counts[p] for p in counts)
-    roofline["read_ceiling"] = {
-        "step_ms": round(ceil_step_us / 1e3, 4),
-        "frac_of_peak": round(step_bytes / ceil_step_us / 1e3 / HBM_PEAK_GBS, 4),
-        "note": "the step's 129 launches priced at the read-only probe's time for each size",
-        "per_shape": per_shape}
+    rceil = read_ceiling(torch, sq8, dev, shape_bytes) if not args.no_ceiling else None
+    if rceil is not None:
+        cceil = copy_ceiling(torch, dev, shape_bytes)
+        gemv_us = {r["proj"]: r["us"] for r in sweep if r["M"] == 1}
+        counts = {p: LAYERS for p in PROJ}
+        counts["lm_head"] = 1
+        per_shape = {}
+        for p, nb in shape_bytes:
+            rec = {"algo_bytes": nb, "read_probe_us": rceil[p]["us"], "copy_us": cceil[p]["us"],
+                   "read_probe_setting": [rceil[p]["workgroups_per_cu"],
+                                          rceil[p]["chunks_per_lane"]]}
+            if p in gemv_us:
+                rec["gemv_us"] = gemv_us[p]
+                rec["gemv_GBps"] = round(nb / gemv_us[p] / 1e3, 1)
+                rec["gemv_frac_of_peak"] = round(nb / gemv_us[p] / 1e3 / HBM_PEAK_GBS, 4)
+                rec["gemv_frac_of_read_probe"] = round(rceil[p]["us"] / gemv_us[p], 3)
+            per_shape[p] = rec
+        ceil_step_us = sum(rceil[p]["us"] * counts[p] for p in counts)
+        roofline["read_ceiling"] = {
+            "step_ms": round(ceil_step_us / 1e3, 4),
+            "frac_of_peak": round(step_bytes / ceil_step_us / 1e3 / HBM_PEAK_GBS, 4),
+            "note": "the step's 129 launches priced at the read-only probe's time for each size",
+            "per_shape": per_shape}
 
     llama = None
     if not args.no_llama_decode:

@@ -241,14 +241,15 @@ struct PTile {
 // GM M-tiles (column by column within a band): the ~32 workgroups an XCD runs at once then
 // share GM activation tiles and 32 / GM weight tiles in its L2, where launch order spread every
 // N-tile over all 8 XCDs and each M-tile over several. A bijection when the grid is a multiple
-// of 8 workgroups; otherwise the launch order is kept.
+// of 8 workgroups; otherwise, and for a single M-tile, the launch order is kept.
 __device__ __forceinline__ void gemm_tile_coords(int& bx, int& by, int& bz) {
   const int X = gridDim.x, Y = gridDim.y, Z = gridDim.z;
   const int total = X * Y * Z;
   const int b = blockIdx.x + X * (blockIdx.y + Y * blockIdx.z);
   bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
   constexpr int GM = SQ8_GEMM_GM;
-  if (GM <= 0 || total % 8 != 0) return;
+  // A single M-tile (the weight-streaming 64-row tiles) keeps the launch order.
+  if (GM <= 0 || Y == 1 || total % 8 != 0) return;
   const int L = (b & 7) * (total >> 3) + (b >> 3);
   const int XY = X * Y;
   bz = L / XY;
