@@ -487,6 +487,18 @@ namespace {
 #ifndef SQ8_GEMV_PAIR_WPC
 #define SQ8_GEMV_PAIR_WPC 16
 #endif
+#ifndef SQ8_GEMV_SPLITROW_WV
+#define SQ8_GEMV_SPLITROW_WV 16
+#endif
+#ifndef SQ8_GEMV_SPLITROW_U
+#define SQ8_GEMV_SPLITROW_U 5
+#endif
+#ifndef SQ8_GEMV_SPLITROW_KS
+#define SQ8_GEMV_SPLITROW_KS 2
+#endif
+#ifndef SQ8_GEMV_PAIR_U1536
+#define SQ8_GEMV_PAIR_U1536 2
+#endif
 
 // LDS bytes the stream kernel may use for staged token rows (MT * K fp32).
 constexpr size_t kStreamLdsMax = 64 * 1024;
@@ -567,6 +579,13 @@ hipError_t launch_stream(const float* x, const int8_t* w, const float* s, float*
   // 8-wave split-row workgroups, twice as many, the decode step measured slower).
   if (MT == 1 && PRO != kProNone && N <= 2048 && K >= 8192 && K <= 10 * 1024)
     return launch_splitrow<5, 2, 16, PRO>(x, w, s, y, N, K, gs, st, pro);
+  // The same few long rows without a prologue (Qwen2-1.5B down projection behind the SwiGLU
+  // epilogue of gate/up): two waves per row, SQ8_GEMV_SPLITROW_WV waves per workgroup.
+#if SQ8_GEMV_SPLITROW_WV > 0
+  if (MT == 1 && PRO == kProNone && N <= 2048 && K >= 8192 && K <= 10 * 1024)
+    return launch_splitrow<SQ8_GEMV_SPLITROW_U, SQ8_GEMV_SPLITROW_KS, SQ8_GEMV_SPLITROW_WV, PRO>(
+        x, w, s, y, N, K, gs, st, pro);
+#endif
   if (K >= 8192) {
     return K % 7168 == 0 ? launch_sweep<1, 7, 16, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro)
                          : launch_sweep<1, 4, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
@@ -646,8 +665,10 @@ hipError_t launch_gemv_norm_swiglu(const float* x, const float* res, float* x_ou
   const int wpc = SQ8_GEMV_PAIR_WPC;
   if (K <= 1024)
     return launch_sweep<2, 1, WV, 1, kProNorm, true>(x, w, s, y, 1, N, K, gs, st, pro, wpc);
-  if (K <= 2048)
+  if (K <= 2048 && (SQ8_GEMV_PAIR_U1536 == 2 || K % 1024 == 0))
     return launch_sweep<2, 2, WV, 1, kProNorm, true>(x, w, s, y, 1, N, K, gs, st, pro, wpc);
+  if (K <= 2048)
+    return launch_sweep<2, 1, WV, 1, kProNorm, true>(x, w, s, y, 1, N, K, gs, st, pro, wpc);
   return launch_sweep<2, 4, WV, 1, kProNorm, true>(x, w, s, y, 1, N, K, gs, st, pro, wpc);
 }
 

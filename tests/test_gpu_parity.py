@@ -55,7 +55,7 @@ def test_small_shapes(sq8, dev, M, N, K):
 @pytest.mark.parametrize("M", [1, 2, 4])
 @pytest.mark.parametrize("N,K,gs", [(33, 8192, 64), (50, 9280, 64), (17, 14336, 64),
                                     (9, 14336, 32), (21, 16000, 64), (300, 7168, 64),
-                                    (19, 20480, 64)])
+                                    (19, 20480, 64), (1536, 8960, 64), (2048, 10240, 32)])
 def test_long_rows_decode(sq8, dev, M, N, K, gs):
     """Decode rows of 7-20 K elements: one-row-per-wave configurations, with and without a
     partial last step, two token rows staged in up to 128 KiB of LDS, and rows whose staged
