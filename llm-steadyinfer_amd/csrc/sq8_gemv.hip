@@ -478,6 +478,16 @@ int cu_count() {
 
 namespace {
 
+// Launch configurations measured best on MI355X (Llama-3-8B and Qwen2-1.5B decode steps; the
+// values are macros so that variants can be built for A/B runs without editing the dispatch):
+//   NARROW_WPC      resident waves per CU for N <= 8192 (12, 24 and 32 measured slower);
+//   PAIR_WV, _WPC   the row-pair (gate/up + SwiGLU) GEMV: 8-wave workgroups, 16 waves per CU
+//                   (4-wave: 22.6 -> 23.7 us on Llama gate/up; 7 waves: 35 us; 24-32 per CU slower);
+//   PAIR_U1536      1 KiB steps per row for 1024 < K <= 2048 when 1: 2 (one masked 2 KiB step
+//                   for K = 1536) measured faster;
+//   SPLITROW_*      two waves per row (U chunks of 1 KiB each) in 16-wave workgroups for the plain
+//                   few-long-rows shape (Qwen2 down: 1122 against 1056 tokens/s unsplit; 3 or 4
+//                   waves per row, 8- or 15-wave workgroups, one wave of 9 chunks all slower).
 #ifndef SQ8_GEMV_NARROW_WPC
 #define SQ8_GEMV_NARROW_WPC 16
 #endif
@@ -487,6 +497,9 @@ namespace {
 #ifndef SQ8_GEMV_PAIR_WPC
 #define SQ8_GEMV_PAIR_WPC 16
 #endif
+#ifndef SQ8_GEMV_PAIR_U1536
+#define SQ8_GEMV_PAIR_U1536 2
+#endif
 #ifndef SQ8_GEMV_SPLITROW_WV
 #define SQ8_GEMV_SPLITROW_WV 16
 #endif
@@ -495,9 +508,6 @@ namespace {
 #endif
 #ifndef SQ8_GEMV_SPLITROW_KS
 #define SQ8_GEMV_SPLITROW_KS 2
-#endif
-#ifndef SQ8_GEMV_PAIR_U1536
-#define SQ8_GEMV_PAIR_U1536 2
 #endif
 
 // LDS bytes the stream kernel may use for staged token rows (MT * K fp32).
