@@ -1134,8 +1134,8 @@ __global__ __launch_bounds__(W * kWave) void tile_kernel(
   constexpr int OUTS = RT * T * 4 * kWave;  // accumulator floats per wave
   constexpr int NT = W * kWave;
   constexpr int SROWS = 16 * T;             // weight rows (output columns) of the workgroup
-  constexpr int LDSF = (W > 1 ? W * OUTS : 0) > SROWS * kTileScaleGroups
-                           ? W * OUTS : SROWS * kTileScaleGroups;
+  constexpr int LDSF = (W > 1 ? W * OUTS : 0) > SROWS * (kTileScaleGroups + 1)
+                           ? W * OUTS : SROWS * (kTileScaleGroups + 1);
   static_assert(LDSF * 4 <= 64 * 1024, "tile_kernel LDS above 64 KiB");
   // Scale stage [SROWS][gps] during the main loop, then the cross-wave reduction buffer.
   __shared__ float lds[LDSF];
@@ -1149,13 +1149,14 @@ __global__ __launch_bounds__(W * kWave) void tile_kernel(
   const int gsplit = blockIdx.y * gps;              // first group of this split
   const int gcount = min(G, gsplit + gps) - gsplit; // groups in this split (<= kTileScaleGroups)
   const int nst = wave < gcount ? (gcount - wave + W - 1) / W : 0;
+  const int sstride = gcount + 1;  // padded: the 16 lanes of a column read distinct banks
 
   // Stage the split's scales of the workgroup's rows in LDS: row-contiguous, coalesced loads.
   // Per-lane loads in the MFMA layout would touch 16 rows per instruction, once per group.
   for (int idx = tid; idx < SROWS * gcount; idx += NT) {
     const int r = idx / gcount, gi = idx - r * gcount;
     const int n = min(n0 + r, N - 1);
-    lds[r * gcount + gi] = s[static_cast<size_t>(n) * gpr + ((gsplit + gi) * BK) / gs];
+    lds[r * sstride + gi] = s[static_cast<size_t>(n) * gpr + ((gsplit + gi) * BK) / gs];
   }
 
   const int8_t* wrow[T];
@@ -1206,7 +1207,7 @@ __global__ __launch_bounds__(W * kWave) void tile_kernel(
       const u32x4 b1 = {hq[4], hq[5], hq[6], hq[7]};
       bw[j][0] = __builtin_bit_cast(h8, b0);
       bw[j][1] = __builtin_bit_cast(h8, b1);
-      const float v = lds[(16 * j + lcol) * gcount + gi_b[b]];
+      const float v = lds[(16 * j + lcol) * sstride + gi_b[b]];
       sc[j] = live_b[b] ? v : 0.f;
     }
 #pragma unroll

@@ -88,7 +88,10 @@ class Int8Decoder:
         cfg, gs = m.config, m.group_size
 
         def dev(a, dtype):
-            return torch.from_numpy(np.ascontiguousarray(a)).to(device=device, dtype=dtype)
+            a = np.ascontiguousarray(a)
+            if not a.flags.writeable:      # a read-only memmap view: stage through a host copy
+                a = a.copy()
+            return torch.from_numpy(a).to(device=device, dtype=dtype)
 
         def fused(names, layer):
             qs, ss = zip(*(m.quant(n, layer) for n in names))
