@@ -53,6 +53,27 @@ int sq8_matmul(const float* x, const int8_t* w, const float* scales, float* y, i
  * split-K partials here. */
 size_t sq8_workspace_bytes(int M, int N, int K, int group_size);
 
+/* Packed weights. sq8_pack_weights rewrites a row-major int8 weight [N][K] (K % 64 == 0) into
+ * 16-row tiles whose 16 x 64 blocks are stored contiguously, 1 KiB each, in the order the
+ * matrix-core kernels load them: byte 16 L + b of block (t, g) is w[16 t + L % 16][64 g +
+ * 16 (L / 16) + b]; a tile's K / 64 blocks follow one another, tiles in order, and the rows past N
+ * are zero. The scales keep their layout. The reference keeps one row-major layout
+ * (layer.cpp:174-231, uploaded by LayerParam::to_cuda); this is an upload-time transform with no
+ * reference counterpart, for callers that repack once and keep only the packed copy. Each
+ * _packed entry point below computes what its row-major counterpart computes:
+ *   - from 3 token rows on, the same kernels with packed addressing: bit-identical results;
+ *   - at 1-2 rows (group size 64, K % 256 == 0, 16-byte aligned scales) a packed GEMV whose
+ *     summation order differs from the row-major GEMV's (same tolerance to the reference);
+ *     other 1-2-row shapes take the int8-limb matrix-core kernel.
+ * Requirements: K % 64 == 0, group_size % 64 == 0 and divides K, 16-byte aligned x and packed
+ * weights, and a workspace of the _workspace_bytes size (never NULL: the ticket area). */
+size_t sq8_packed_weight_bytes(int N, int K);
+int sq8_pack_weights(const int8_t* w, int N, int K, int8_t* packed, void* hip_stream);
+size_t sq8_packed_workspace_bytes(int M, int N, int K, int group_size);
+int sq8_matmul_packed(const float* x, const int8_t* packed, const float* scales, float* y, int M,
+                      int N, int K, int group_size, void* workspace, size_t workspace_bytes,
+                      void* hip_stream);
+
 /* Output epilogues of sq8_matmul_epilogue. */
 enum sq8_epilogue {
   SQ8_EPI_NONE = 0,      /* y[M][N] = x . W^T (as sq8_matmul) */
@@ -94,6 +115,20 @@ size_t sq8_rmsnorm_rows_workspace_bytes(int M, int N, int K, int group_size, int
 
 /* 1 if sq8_matmul_epilogue fuses the epilogue into the matmul kernel for this shape, else 0. */
 int sq8_epilogue_fused(int M, int N, int K, int group_size);
+
+/* The epilogue and RMSNorm-rows entry points on packed weights (see sq8_pack_weights above). */
+int sq8_epilogue_packed_fused(int M, int N, int K, int group_size);
+size_t sq8_epilogue_packed_workspace_bytes(int M, int N, int K, int group_size, int epilogue);
+int sq8_matmul_epilogue_packed(const float* x, const int8_t* packed, const float* scales,
+                               float* y, int M, int N, int K, int group_size, int epilogue,
+                               const float* residual, void* workspace, size_t workspace_bytes,
+                               void* hip_stream);
+size_t sq8_rmsnorm_rows_packed_workspace_bytes(int M, int N, int K, int group_size,
+                                               int epilogue);
+int sq8_matmul_rmsnorm_rows_packed(float* x, const float* res, const float* norm_w, float eps,
+                                   const int8_t* packed, const float* scales, float* y, int M,
+                                   int N, int K, int group_size, int epilogue, void* workspace,
+                                   size_t workspace_bytes, void* hip_stream);
 
 /* Size of the device scratch array behind sq8_matmul_noalloc (32 MiB per GPU). */
 #define SQ8_NOALLOC_SCRATCH_BYTES (32u * 1024u * 1024u)

@@ -25,7 +25,11 @@ EXPORTED_SYMBOLS = ("sq8_matmul", "sq8_workspace_bytes", "sq8_status_string", "s
                     "sq8_matmul_epilogue", "sq8_epilogue_workspace_bytes", "sq8_epilogue_fused",
                     "sq8_matmul_rmsnorm_rows", "sq8_rmsnorm_rows_fused",
                     "sq8_rmsnorm_rows_workspace_bytes", "sq8_matmul_noalloc",
-                    "sq8_noalloc_scratch_bytes")
+                    "sq8_noalloc_scratch_bytes", "sq8_packed_weight_bytes", "sq8_pack_weights",
+                    "sq8_packed_workspace_bytes", "sq8_matmul_packed",
+                    "sq8_epilogue_packed_fused", "sq8_epilogue_packed_workspace_bytes",
+                    "sq8_matmul_epilogue_packed", "sq8_rmsnorm_rows_packed_workspace_bytes",
+                    "sq8_matmul_rmsnorm_rows_packed")
 
 # Output epilogues (include/sq8.h, enum sq8_epilogue).
 SQ8_EPI_NONE = 0
@@ -82,6 +86,20 @@ def lib() -> ctypes.CDLL:
         L.sq8_rmsnorm_rows_fused.restype = I
         L.sq8_rmsnorm_rows_workspace_bytes.argtypes = [I, I, I, I, I]
         L.sq8_rmsnorm_rows_workspace_bytes.restype = sz
+        L.sq8_packed_weight_bytes.argtypes = [I, I]
+        L.sq8_packed_weight_bytes.restype = sz
+        L.sq8_pack_weights.argtypes = [vp, I, I, vp, vp]
+        L.sq8_packed_workspace_bytes.argtypes = [I, I, I, I]
+        L.sq8_packed_workspace_bytes.restype = sz
+        L.sq8_matmul_packed.argtypes = [vp, vp, vp, vp, I, I, I, I, vp, sz, vp]
+        L.sq8_epilogue_packed_fused.argtypes = [I, I, I, I]
+        L.sq8_epilogue_packed_workspace_bytes.argtypes = [I, I, I, I, I]
+        L.sq8_epilogue_packed_workspace_bytes.restype = sz
+        L.sq8_matmul_epilogue_packed.argtypes = [vp, vp, vp, vp, I, I, I, I, I, vp, vp, sz, vp]
+        L.sq8_rmsnorm_rows_packed_workspace_bytes.argtypes = [I, I, I, I, I]
+        L.sq8_rmsnorm_rows_packed_workspace_bytes.restype = sz
+        L.sq8_matmul_rmsnorm_rows_packed.argtypes = [vp, vp, vp, ctypes.c_float, vp, vp, vp, I,
+                                                     I, I, I, I, vp, sz, vp]
         L.sq8_epilogue_fused.argtypes = [I, I, I, I]
         L.sq8_epilogue_fused.restype = I
         f32 = ctypes.c_float
@@ -165,6 +183,39 @@ class Workspace:
 _default_ws = {}
 
 
+class PackedWeight:
+    """An INT8 weight [N][K] in the packed layout of sq8_pack_weights (16-row tiles, each 64-wide
+    group of a tile one contiguous 1 KiB block). Accepted wherever a row-major int8 weight is:
+    matmul, matmul_epilogue and matmul_rmsnorm_rows then call the _packed entry points."""
+
+    def __init__(self, data, N: int, K: int):
+        self.data, self.N, self.K = data, N, K
+        self.shape = (N, K)
+        self.device = data.device
+
+    def data_ptr(self) -> int:
+        return self.data.data_ptr()
+
+    def is_contiguous(self) -> bool:
+        return True
+
+
+def pack_weights(w, stream=None) -> PackedWeight:
+    """Repack a row-major int8 weight [N][K] (K % 64 == 0) on the GPU (sq8_pack_weights)."""
+    import torch
+    N, K = w.shape
+    if not w.is_contiguous():
+        raise ValueError("sq8 tensors must be contiguous")
+    data = torch.empty(int(lib().sq8_packed_weight_bytes(N, K)), dtype=torch.int8,
+                       device=w.device)
+    if stream is None:
+        stream = torch.cuda.current_stream(w.device)
+    rc = int(lib().sq8_pack_weights(w.data_ptr(), N, K, data.data_ptr(), stream.cuda_stream))
+    if rc != SQ8_OK:
+        raise Sq8Error(rc)
+    return PackedWeight(data, N, K)
+
+
 def matmul(x, w, scales, y=None, group_size: int = 64, workspace: Workspace | None = None,
            stream=None):
     """y[M,N] = x[M,K] @ dequant(w[N,K], scales).T on the current torch stream.
@@ -184,15 +235,23 @@ def matmul(x, w, scales, y=None, group_size: int = 64, workspace: Workspace | No
         stream = torch.cuda.current_stream(x.device)
     if workspace is None:
         workspace = _default_ws.setdefault(str(x.device), Workspace(x.device))
-    ws_ptr, ws_n = workspace.get(workspace_bytes(M, N, K, group_size))
-    rc = matmul_raw(x2.data_ptr(), w.data_ptr(), scales.data_ptr(), y.data_ptr(), M, N, K,
-                    group_size, ws_ptr, ws_n, stream.cuda_stream)
+    if isinstance(w, PackedWeight):
+        ws_ptr, ws_n = workspace.get(int(lib().sq8_packed_workspace_bytes(M, N, K, group_size)))
+        rc = int(lib().sq8_matmul_packed(x2.data_ptr(), w.data_ptr(), scales.data_ptr(),
+                                         y.data_ptr(), M, N, K, group_size, ws_ptr or None, ws_n,
+                                         stream.cuda_stream))
+    else:
+        ws_ptr, ws_n = workspace.get(workspace_bytes(M, N, K, group_size))
+        rc = matmul_raw(x2.data_ptr(), w.data_ptr(), scales.data_ptr(), y.data_ptr(), M, N, K,
+                        group_size, ws_ptr, ws_n, stream.cuda_stream)
     if rc != SQ8_OK:
         raise Sq8Error(rc)
     return y.reshape(-1) if squeeze else y
 
 
-def epilogue_fused(M: int, N: int, K: int, group_size: int = 64) -> bool:
+def epilogue_fused(M: int, N: int, K: int, group_size: int = 64, packed: bool = False) -> bool:
+    if packed:
+        return bool(lib().sq8_epilogue_packed_fused(M, N, K, group_size))
     return bool(lib().sq8_epilogue_fused(M, N, K, group_size))
 
 
@@ -212,11 +271,13 @@ def matmul_epilogue(x, w, scales, y, epilogue: int, residual=None, group_size: i
         stream = torch.cuda.current_stream(x.device)
     if workspace is None:
         workspace = _default_ws.setdefault(str(x.device), Workspace(x.device))
-    ws_ptr, ws_n = workspace.get(int(lib().sq8_epilogue_workspace_bytes(M, N, K, group_size,
-                                                                         epilogue)))
-    rc = int(lib().sq8_matmul_epilogue(x.data_ptr(), w.data_ptr(), scales.data_ptr(),
-                                       y.data_ptr(), M, N, K, group_size, epilogue,
-                                       _ptr(residual), ws_ptr or None, ws_n, stream.cuda_stream))
+    pk = isinstance(w, PackedWeight)
+    need = (lib().sq8_epilogue_packed_workspace_bytes if pk
+            else lib().sq8_epilogue_workspace_bytes)(M, N, K, group_size, epilogue)
+    ws_ptr, ws_n = workspace.get(int(need))
+    fn = lib().sq8_matmul_epilogue_packed if pk else lib().sq8_matmul_epilogue
+    rc = int(fn(x.data_ptr(), w.data_ptr(), scales.data_ptr(), y.data_ptr(), M, N, K, group_size,
+                epilogue, _ptr(residual), ws_ptr or None, ws_n, stream.cuda_stream))
     if rc != SQ8_OK:
         raise Sq8Error(rc)
     return y
@@ -242,12 +303,14 @@ def matmul_rmsnorm_rows(x, res, norm_w, eps: float, w, scales, y, epilogue: int 
         stream = torch.cuda.current_stream(x.device)
     if workspace is None:
         workspace = _default_ws.setdefault(str(x.device), Workspace(x.device))
-    ws_ptr, ws_n = workspace.get(int(lib().sq8_rmsnorm_rows_workspace_bytes(M, N, K, group_size,
-                                                                             epilogue)))
-    rc = int(lib().sq8_matmul_rmsnorm_rows(x.data_ptr(), _ptr(res), norm_w.data_ptr(), eps,
-                                           w.data_ptr(), scales.data_ptr(), y.data_ptr(), M, N,
-                                           K, group_size, epilogue, ws_ptr or None, ws_n,
-                                           stream.cuda_stream))
+    pk = isinstance(w, PackedWeight)
+    need = (lib().sq8_rmsnorm_rows_packed_workspace_bytes if pk
+            else lib().sq8_rmsnorm_rows_workspace_bytes)(M, N, K, group_size, epilogue)
+    ws_ptr, ws_n = workspace.get(int(need))
+    fn = lib().sq8_matmul_rmsnorm_rows_packed if pk else lib().sq8_matmul_rmsnorm_rows
+    rc = int(fn(x.data_ptr(), _ptr(res), norm_w.data_ptr(), eps, w.data_ptr(), scales.data_ptr(),
+                y.data_ptr(), M, N, K, group_size, epilogue, ws_ptr or None, ws_n,
+                stream.cuda_stream))
     if rc != SQ8_OK:
         raise Sq8Error(rc)
     return y

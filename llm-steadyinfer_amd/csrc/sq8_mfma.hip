@@ -264,7 +264,8 @@ __device__ __forceinline__ void gemm_tile_coords(int& bx, int& by, int& bz) {
 template <int WAVES_M, int WAVES_N, int TM, int TN, int STAGES, int GPS>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
     const _Float16* xh, const _Float16* xl, const float* __restrict__ rscale, const int8_t* w,
-    const float* s, float* out, int M, int N, int K, int gs, int groups_per_split, Epi epi) {
+    const float* s, float* out, int M, int N, int K, int gs, int groups_per_split, Epi epi,
+    int pk) {
   using T = PTile<WAVES_M, WAVES_N, TM, TN, STAGES, GPS>;
   static_assert(TN % 2 == 0, "SwiGLU pairs tile j (gate) with tile j + TN/2 (up) of a wave");
   constexpr int HT = TN / 2;
@@ -307,7 +308,11 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
   for (int i = 0; i < T::WL; ++i) {
     const int slot = (i * T::NW + wave) * kWave + lane;
     const int r = slot / T::CW, q = (slot % T::CW) ^ swz_w<GPS>(slot / T::CW);
-    woff[i] = static_cast<uint32_t>(wrow(r)) * K + q * 16u;
+    const uint32_t n = static_cast<uint32_t>(wrow(r));
+    // Packed: chunk q of the stage is chunk q % 4 of its group q / 4, in the row's tile block.
+    woff[i] = pk ? (n >> 4) * static_cast<uint32_t>(K) * 16u + (q >> 2) * 1024u +
+                       (((q & 3) * 16u + (n & 15u)) * 16u)
+                 : n * K + q * 16u;
   }
 #pragma unroll
   for (int i = 0; i < T::SL; ++i) {
@@ -319,7 +324,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
     const uint32_t sb = lds0 + buf * T::STAGE;
     const char* xhb = reinterpret_cast<const char*>(xh) + static_cast<size_t>(st) * T::KB * 2;
     const char* xlb = reinterpret_cast<const char*>(xl) + static_cast<size_t>(st) * T::KB * 2;
-    const char* wb = reinterpret_cast<const char*>(w) + static_cast<size_t>(st) * T::KB;
+    const char* wb = reinterpret_cast<const char*>(w) +
+                     static_cast<size_t>(st) * (pk ? GPS * 1024 : T::KB);
 #pragma unroll
     for (int i = 0; i < T::XL; ++i) {
       const uint32_t d = ((i * T::NW + wave) * kWave) * 16;
@@ -562,7 +568,7 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 template <int MR, int KW, int TN, int MT16, bool F4>
 __global__ __launch_bounds__(kThreads) void skinny16_kernel(
     const float* x, const int8_t* w, const float* s, float* __restrict__ y, float* __restrict__ part, unsigned* __restrict__ tickets, int M, int N,
-    int K, int gs, int gps, int splits) {
+    int K, int gs, int gps, int splits, int pk) {
   constexpr int BMP = 16 * MT16;                   // MFMA rows: MT16 stacked 16-row tiles
   static_assert(MR <= BMP && (MR == 8 || MR % 16 == 0), "rows loaded per chunk");
   constexpr int BN = 4 * TN * 16;                  // 4 waves x TN tiles of 16 columns
@@ -580,6 +586,7 @@ __global__ __launch_bounds__(kThreads) void skinny16_kernel(
   const int gbeg = blockIdx.y * gps;
   const int nch = (min(K / BK, gbeg + gps) - gbeg) / KW;
   const int gpr = K / gs;
+  const int gstep = wgroup_step(pk);
 
   if (MR < BMP) {  // rows MR..15 of both buffers are never loaded: zero them once
     for (int i = tid; i < 2 * KW * (BMP - MR) * LDS_STRIDE; i += kThreads) {
@@ -599,7 +606,7 @@ __global__ __launch_bounds__(kThreads) void skinny16_kernel(
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int ncol = min(n0 + (wave * TN + j) * 16 + lcol, N - 1);
-    wsrc[j] = w + static_cast<size_t>(ncol) * K + static_cast<size_t>(gbeg) * BK + kq;
+    wsrc[j] = lane_wbase(w, pk, ncol, K, lane) + static_cast<size_t>(gbeg) * gstep;
     ssrc[j] = s + static_cast<size_t>(ncol) * gpr;
   }
 
@@ -611,7 +618,7 @@ __global__ __launch_bounds__(kThreads) void skinny16_kernel(
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         wr[b][q][j] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(wsrc[j] + (c * KW + q) * BK));
+            reinterpret_cast<const u32x4*>(wsrc[j] + (c * KW + q) * gstep));
         if constexpr (!F4) wsc[b][q][j] = ssrc[j][((gbeg + c * KW + q) * BK) / gs];
       }
     if constexpr (F4) {  // group_size 64, KW == 4: the chunk's 4 scales of a row are one float4
@@ -819,7 +826,7 @@ constexpr int kLimbRowBytes = 80;  // 64 limb bytes + 16 padding: conflict-free 
 template <int NB, int KW, int TN, bool F4>
 __global__ __launch_bounds__(kThreads) void skinny_i8_kernel(
     const float* x, const int8_t* w, const float* s, float* __restrict__ y, float* __restrict__ part, unsigned* __restrict__ tickets, int M, int N,
-    int K, int gs, int gps, int splits) {
+    int K, int gs, int gps, int splits, int pk) {
   constexpr int MT = 4 * NB;                       // token slots
   constexpr int ROWS = 16 * NB;                    // A rows (4 limbs per token)
   constexpr int BN = 4 * TN * 16;                  // 4 waves x TN tiles of 16 columns
@@ -837,13 +844,14 @@ __global__ __launch_bounds__(kThreads) void skinny_i8_kernel(
   const int gbeg = blockIdx.y * gps;
   const int nch = (min(K / BK, gbeg + gps) - gbeg) / KW;
   const int gpr = K / gs;
+  const int gstep = wgroup_step(pk);
 
   const int8_t* wsrc[TN];
   const float* ssrc[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int ncol = min(n0 + (wave * TN + j) * 16 + lcol, N - 1);
-    wsrc[j] = w + static_cast<size_t>(ncol) * K + static_cast<size_t>(gbeg) * BK + kq;
+    wsrc[j] = lane_wbase(w, pk, ncol, K, lane) + static_cast<size_t>(gbeg) * gstep;
     ssrc[j] = s + static_cast<size_t>(ncol) * gpr;
   }
 
@@ -855,7 +863,7 @@ __global__ __launch_bounds__(kThreads) void skinny_i8_kernel(
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         wr[b][q][j] = __builtin_nontemporal_load(
-            reinterpret_cast<const i32x4v*>(wsrc[j] + (c * KW + q) * BK));
+            reinterpret_cast<const i32x4v*>(wsrc[j] + (c * KW + q) * gstep));
         if constexpr (!F4) wsc[b][q][j] = ssrc[j][((gbeg + c * KW + q) * BK) / gs];
       }
     if constexpr (F4) {  // group_size 64, KW == 4: the chunk's 4 scales of a row are one float4
@@ -1130,7 +1138,7 @@ template <int RT, int T, int W>
 __global__ __launch_bounds__(W * kWave) void tile_kernel(
     const u32x4* xp, const float* __restrict__ rscale, const int8_t* w, const float* s,
     float* __restrict__ y, float* __restrict__ part,
-    unsigned* __restrict__ tickets, int M, int N, int K, int gs, int gps, int splits) {
+    unsigned* __restrict__ tickets, int M, int N, int K, int gs, int gps, int splits, int pk) {
   constexpr int OUTS = RT * T * 4 * kWave;  // accumulator floats per wave
   constexpr int NT = W * kWave;
   constexpr int SROWS = 16 * T;             // weight rows (output columns) of the workgroup
@@ -1143,7 +1151,7 @@ __global__ __launch_bounds__(W * kWave) void tile_kernel(
 
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lcol = lane & 15, kq = (lane >> 4) * 16;
+  const int lcol = lane & 15;
   const int n0 = blockIdx.x * (16 * T);
   const int G = K / BK, gpr = K / gs;
   const int gsplit = blockIdx.y * gps;              // first group of this split
@@ -1162,7 +1170,8 @@ __global__ __launch_bounds__(W * kWave) void tile_kernel(
   const int8_t* wrow[T];
 #pragma unroll
   for (int j = 0; j < T; ++j)
-    wrow[j] = w + static_cast<size_t>(min(n0 + 16 * j + lcol, N - 1)) * K + kq;
+    wrow[j] = lane_wbase(w, pk, min(n0 + 16 * j + lcol, N - 1), K, lane);
+  const int gstep = wgroup_step(pk);
   const u32x4* xlane = xp + lane;
 
   // Wave w takes groups w, w + W, ... of the split: the W waves of a workgroup read neighbouring
@@ -1178,7 +1187,7 @@ __global__ __launch_bounds__(W * kWave) void tile_kernel(
 #pragma unroll
     for (int j = 0; j < T; ++j)
       bq[b][j] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(wrow[j] + static_cast<size_t>(g) * BK));
+          reinterpret_cast<const u32x4*>(wrow[j] + static_cast<size_t>(g) * gstep));
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
@@ -1346,7 +1355,7 @@ __global__ __launch_bounds__(W * kWave) void tile_kernel(
 template <int RT, int T, int W, int D>
 __global__ __launch_bounds__(W * kWave) void dgemm_kernel(
     const u32x4* xp, const float* __restrict__ rscale, const int8_t* w, const float* s,
-    float* out, int M, int N, int K, int gs, int gps, Epi epi) {
+    float* out, int M, int N, int K, int gs, int gps, Epi epi, int pk) {
   constexpr int XSTAGE = RT * 4 * kWave * 16;          // bytes of one group's fragments
   constexpr int NCH = XSTAGE / (kWave * 16);           // 1 KiB chunks of a group's fragments
   constexpr int LXD = (NCH + W - 1) / W;               // DMA instructions per thread per group
@@ -1359,7 +1368,7 @@ __global__ __launch_bounds__(W * kWave) void dgemm_kernel(
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lcol = lane & 15, kq = (lane >> 4) * 16;
+  const int lcol = lane & 15;
   const int G = K / BK, gpr = K / gs;
   const int gsplit = blockIdx.y * gps;
   const int gcount = min(G, gsplit + gps) - gsplit;
@@ -1383,7 +1392,8 @@ __global__ __launch_bounds__(W * kWave) void dgemm_kernel(
   const int8_t* wr[T];
 #pragma unroll
   for (int j = 0; j < T; ++j)
-    wr[j] = w + static_cast<size_t>(wrow((wave * T + j) * 16 + lcol)) * K + kq;
+    wr[j] = lane_wbase(w, pk, wrow((wave * T + j) * 16 + lcol), K, lane);
+  const int gstep = wgroup_step(pk);
   const float* scol[T];
 #pragma unroll
   for (int j = 0; j < T; ++j) scol[j] = sscale + ((wave * T + j) * 16 + lcol) * sstride;
@@ -1410,7 +1420,7 @@ __global__ __launch_bounds__(W * kWave) void dgemm_kernel(
     for (int j = 0; j < T; ++j)
       asm volatile("global_load_dwordx4 %0, %1, off nt"
                    : "=v"(wq[slot][j])
-                   : "v"(wr[j] + static_cast<size_t>(g) * BK)
+                   : "v"(wr[j] + static_cast<size_t>(g) * gstep)
                    : "memory");
   };
   auto tie = [&](int slot) __attribute__((always_inline)) {
@@ -1689,7 +1699,7 @@ Plan make_plan(int M, int N, int K) {
 template <int WM, int WN, int TM, int TN, int STAGES, int GPS = 1>
 hipError_t launch_gemm(const _Float16* xh, const _Float16* xl, const float* rsc,
                             const int8_t* w, const float* s, float* out, int M, int N, int K,
-                            int gs, const Plan& p, hipStream_t st, Epi epi) {
+                            int gs, const Plan& p, hipStream_t st, Epi epi, int pk) {
   using T = PTile<WM, WN, TM, TN, STAGES, GPS>;
   auto kern = gemm_kernel<WM, WN, TM, TN, STAGES, GPS>;
   static std::atomic<uint64_t> done{0};  // LDS above 64 KiB needs the opt-in attribute
@@ -1700,47 +1710,47 @@ hipError_t launch_gemm(const _Float16* xh, const _Float16* xl, const float* rsc,
                                           : (N + T::BN - 1) / T::BN;
   const dim3 grid(cols, (M + T::BM - 1) / T::BM, p.splits);
   hipLaunchKernelGGL(kern, grid, dim3(T::NT), T::LDS_BYTES, st, xh, xl, rsc, w, s, out, M, N, K,
-                     gs, p.groups_per_split, epi);
+                     gs, p.groups_per_split, epi, pk);
   return hipGetLastError();
 }
 
 template <int MR, int KW, int TN = 1, int MT16 = 1>
 hipError_t launch_skinny16(const float* x, const int8_t* w, const float* s, float* y, float* part,
                            unsigned* tickets, int M, int N, int K, int gs, const Plan& p,
-                           hipStream_t st) {
+                           hipStream_t st, int pk) {
   const dim3 grid((N + 64 * TN - 1) / (64 * TN), p.splits);
   // float4 scale loads need 4-group chunks at 16-byte aligned addresses
   const bool f4 = KW == 4 && gs == BK && (K / BK) % 4 == 0 &&
                   (reinterpret_cast<uintptr_t>(s) & 15) == 0;
   if (f4)
     hipLaunchKernelGGL((skinny16_kernel<MR, KW, TN, MT16, KW == 4>), grid, dim3(kThreads), 0, st,
-                       x, w, s, y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits);
+                       x, w, s, y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits, pk);
   else
     hipLaunchKernelGGL((skinny16_kernel<MR, KW, TN, MT16, false>), grid, dim3(kThreads), 0, st, x,
-                       w, s, y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits);
+                       w, s, y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits, pk);
   return hipGetLastError();
 }
 
 template <int NB, int KW, int TN>
 hipError_t launch_skinny_i8(const float* x, const int8_t* w, const float* s, float* y, float* part,
                             unsigned* tickets, int M, int N, int K, int gs, const Plan& p,
-                            hipStream_t st) {
+                            hipStream_t st, int pk) {
   const dim3 grid((N + 64 * TN - 1) / (64 * TN), p.splits);
   const bool f4 = KW == 4 && gs == BK && (K / BK) % 4 == 0 &&
                   (reinterpret_cast<uintptr_t>(s) & 15) == 0;
   if (f4)
     hipLaunchKernelGGL((skinny_i8_kernel<NB, KW, TN, KW == 4>), grid, dim3(kThreads), 0, st, x,
-                       w, s, y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits);
+                       w, s, y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits, pk);
   else
     hipLaunchKernelGGL((skinny_i8_kernel<NB, KW, TN, false>), grid, dim3(kThreads), 0, st, x, w,
-                       s, y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits);
+                       s, y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits, pk);
   return hipGetLastError();
 }
 
 template <int RT>
 hipError_t launch_dgemm(const float* x, const int8_t* w, const float* s, float* y, void* ws, int M,
                         int N, int K, int gs, const Plan& p, hipStream_t st, Epi epi,
-                        const NormArgs* na = nullptr) {
+                        const NormArgs* na, int pk) {
   char* base = static_cast<char*>(ws) + kTicketBytes;
   u32x4* xp = reinterpret_cast<u32x4*>(base);
   base += align256(static_cast<size_t>(K / BK) * RT * 4 * kWave * sizeof(u32x4));
@@ -1767,7 +1777,7 @@ hipError_t launch_dgemm(const float* x, const int8_t* w, const float* s, float* 
                                           : (N + kDgCols - 1) / kDgCols;
   float* out = p.splits > 1 ? part : y;
   hipLaunchKernelGGL(kern, dim3(cols, p.splits), dim3(kDgW * kWave), lds, st, xp, rsc, w, s,
-                     out, M, N, K, gs, p.groups_per_split, epi);
+                     out, M, N, K, gs, p.groups_per_split, epi, pk);
   e = hipGetLastError();
   if (e != hipSuccess || p.splits == 1) return e;
   const size_t count = static_cast<size_t>(M) * (epi.mode == kEpiSwiglu ? N / 2 : N);
@@ -1780,7 +1790,7 @@ hipError_t launch_dgemm(const float* x, const int8_t* w, const float* s, float* 
 template <int RT, int T, int W>
 hipError_t launch_tile(const float* x, const int8_t* w, const float* s, float* y, void* ws, int M,
                        int N, int K, int gs, const Plan& p, hipStream_t st,
-                       const NormArgs* na = nullptr) {
+                       const NormArgs* na, int pk) {
   unsigned* tickets = static_cast<unsigned*>(ws);
   char* base = static_cast<char*>(ws) + kTicketBytes;
   u32x4* xp = reinterpret_cast<u32x4*>(base);
@@ -1798,8 +1808,186 @@ hipError_t launch_tile(const float* x, const int8_t* w, const float* s, float* y
   if (e != hipSuccess) return e;
   const dim3 grid((N + 16 * T - 1) / (16 * T), p.splits);
   hipLaunchKernelGGL((tile_kernel<RT, T, W>), grid, dim3(W * kWave), 0, st, xp, rsc, w, s,
-                     y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits);
+                     y, part, tickets, M, N, K, gs, p.groups_per_split, p.splits, pk);
   return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- packed GEMV (1-2 rows)
+// Weights in the packed layout (lane_wbase). Workgroups are resident for the whole call: each
+// stages x (MT rows of K floats) in LDS once, then its waves walk units in grid stride, with
+// no further barrier. A unit is one 16-row tile and a contiguous slice of KS groups (a KS KiB
+// run of the packed weights); a wave issues U KiB of it per step before using any (latency is
+// hidden by residency, as in the row-major GEMV), and the row's scales of 4 groups arrive as
+// one float4. Per group a lane holds 16 weights of row lane % 16 at k = 64 g + 16 (lane / 16)
+// and multiplies them with the matching 16 activations (float4 LDS reads shared by the 16 lanes
+// of a quarter). The four quarters' sums are added with two lane swaps. With S > 1 slices per
+// tile, each unit stores its 16 x MT sums as a partial and takes a ticket; the last unit of the
+// tile sums the S partials in slice order and resets the ticket.
+constexpr int kPgWaves = 8;
+
+template <int MT, int U>
+__global__ __launch_bounds__(kPgWaves * kWave) void pgemv_kernel(
+    const float* __restrict__ x, const int8_t* w, const float* __restrict__ s,
+    float* __restrict__ y, float* __restrict__ part, unsigned* __restrict__ tickets, int M, int N,
+    int K, int ks, int S) {
+  static_assert(U % 4 == 0, "scales are read as whole float4s");
+  extern __shared__ __attribute__((aligned(16))) float4 xs[];  // [MT][K / 4]
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lcol = lane & 15, q = lane >> 4;
+  const int G = K / BK;
+  const int K4 = K / 4;
+  for (int c = tid; c < MT * K4; c += kPgWaves * kWave) {
+    const int m = c / K4, k4 = c - m * K4;
+    xs[c] = *reinterpret_cast<const float4*>(x + static_cast<size_t>(min(m, M - 1)) * K + 4 * k4);
+  }
+  __syncthreads();
+
+  const int ntiles = (N + 15) / 16;
+  const int units = ntiles * S;
+  for (int u = blockIdx.x * kPgWaves + wave; u < units; u += gridDim.x * kPgWaves) {
+    const int tile = u / S, sl = u - tile * S;
+    const int g0 = sl * ks, gn = min(ks, G - g0);
+    const int8_t* wb = w + static_cast<size_t>(tile) * K * 16 + static_cast<size_t>(g0) * 1024 +
+                       lane * 16;
+    const float* sr = s + static_cast<size_t>(min(tile * 16 + lcol, N - 1)) * G + g0;
+    float acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = 0.f;
+    for (int i0 = 0; i0 < gn; i0 += U) {
+      u32x4 wq[U];
+      float sc[U];
+#pragma unroll
+      for (int v = 0; v < U; ++v)
+        wq[v] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(wb + static_cast<size_t>(min(i0 + v, gn - 1)) * 1024));
+#pragma unroll
+      for (int v = 0; v < U; v += 4) {
+        // gn % 4 == 0 (K % 256 == 0, ks % 4 == 0): the last whole float4 of the slice is
+        // gn - 4; slots past gn read it again and get scale 0 below.
+        const float4 f = *reinterpret_cast<const float4*>(sr + min(i0 + v, gn - 4));
+        sc[v] = f.x;
+        sc[v + 1] = f.y;
+        sc[v + 2] = f.z;
+        sc[v + 3] = f.w;
+      }
+#pragma unroll
+      for (int v = 0; v < U; ++v) {
+        __builtin_amdgcn_sched_barrier(0);  // one group's LDS reads at a time
+        const i32x4 wv = __builtin_bit_cast(i32x4, wq[v]);
+        const int k4 = (g0 + min(i0 + v, gn - 1)) * 16 + q * 4;
+        const float scv = i0 + v < gn ? sc[v] : 0.f;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          const float4* xp = &xs[m * K4 + k4];
+          acc[m] = fmaf(scv, dot16(wv, xp[0], xp[1], xp[2], xp[3]), acc[m]);
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      acc[m] += __shfl_xor(acc[m], 16, kWave);
+      acc[m] += __shfl_xor(acc[m], 32, kWave);
+    }
+    const int n = tile * 16 + lcol;
+    if (S == 1) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        if (lane < 16 && m < M && n < N) y[static_cast<size_t>(m) * N + n] = acc[m];
+      continue;
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+      if (lane < 16 && m < M && n < N)
+        __hip_atomic_store(part + (static_cast<size_t>(sl) * M + m) * N + n, acc[m],
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // The partial stores are acknowledged before the ticket; the last unit of the tile sums
+    // the slices in order.
+    __builtin_amdgcn_s_waitcnt(0);
+    unsigned t = 0;
+    if (lane == 0)
+      t = __hip_atomic_fetch_add(&tickets[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    t = __shfl(t, 0, kWave);
+    if (t != static_cast<unsigned>(S - 1)) continue;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (lane < 16 && m < M && n < N) {
+        float v = 0.f;
+        for (int z = 0; z < S; ++z)
+          v += __hip_atomic_load(part + (static_cast<size_t>(z) * M + m) * N + n,
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        y[static_cast<size_t>(m) * N + n] = v;
+      }
+    }
+    if (lane == 0)
+      __hip_atomic_store(&tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+#ifndef SQ8_PGEMV_U
+#define SQ8_PGEMV_U 4
+#endif
+#ifndef SQ8_PGEMV_WPC
+#define SQ8_PGEMV_WPC 2
+#endif
+struct PgPlan {
+  int ks, S, grid;
+  size_t lds;
+};
+PgPlan pgemv_plan(int M, int N, int K) {
+  PgPlan p{};
+  const int G = K / BK, ntiles = (N + 15) / 16;
+  p.lds = static_cast<size_t>(M) * K * sizeof(float);
+  const int wgs = p.lds > 80 * 1024 ? 1 : SQ8_PGEMV_WPC;  // resident workgroups per CU
+  p.grid = cu_count() * wgs;
+  const int slots = p.grid * kPgWaves;
+  int S = std::max(1, (slots + ntiles - 1) / ntiles);
+  if (ntiles > kTicketBytes / 4) S = 1;
+  int ks = (G + S - 1) / S;
+  ks = std::max(4, (ks + 3) / 4 * 4);  // whole float4s of scales
+  p.ks = ks;
+  p.S = (G + ks - 1) / ks;
+  p.grid = std::min(p.grid, (ntiles * p.S + kPgWaves - 1) / kPgWaves);
+  return p;
+}
+
+template <int MT>
+hipError_t launch_pgemv_mt(const float* x, const int8_t* w, const float* s, float* y, void* ws,
+                           int M, int N, int K, hipStream_t st) {
+  const PgPlan p = pgemv_plan(MT, N, K);
+  auto kern = pgemv_kernel<MT, SQ8_PGEMV_U>;
+  static std::atomic<uint64_t> done{0};
+  if (p.lds > 64 * 1024) {
+    if (p.lds > 144 * 1024) return hipErrorInvalidValue;
+    const hipError_t e = ensure_dynamic_lds(reinterpret_cast<const void*>(kern), 144 * 1024, done);
+    if (e != hipSuccess) return e;
+  }
+  unsigned* tickets = static_cast<unsigned*>(ws);
+  float* part = reinterpret_cast<float*>(static_cast<char*>(ws) + kTicketBytes);
+  hipLaunchKernelGGL(kern, dim3(p.grid), dim3(kPgWaves * kWave), p.lds, st, x, w, s, y, part,
+                     tickets, M, N, K, p.ks, p.S);
+  return hipGetLastError();
+}
+
+#ifndef SQ8_PGEMV_MAX_M
+#define SQ8_PGEMV_MAX_M 2
+#endif
+// Token rows up to which packed weights take the GEMV (above, the int8-limb MFMA kernel).
+constexpr int kPgMaxM = SQ8_PGEMV_MAX_M;
+
+// Packed weights at 1-2 token rows with group size 64 and whole float4s of scales per row.
+bool pgemv_ok(int M, int K, int gs, const float* s) {
+  return M <= kPgMaxM && gs == BK && K % (4 * BK) == 0 &&
+         (reinterpret_cast<uintptr_t>(s) & 15) == 0 &&
+         static_cast<size_t>(M) * K * sizeof(float) <= 144 * 1024;
+}
+
+hipError_t launch_pgemv(const float* x, const int8_t* w, const float* s, float* y, void* ws,
+                        int M, int N, int K, hipStream_t st) {
+  switch (M) {
+    case 1: return launch_pgemv_mt<1>(x, w, s, y, ws, M, N, K, st);
+    default: return launch_pgemv_mt<2>(x, w, s, y, ws, M, N, K, st);
+  }
 }
 
 }  // namespace
@@ -1839,17 +2027,64 @@ bool mfma_norm_fused(int M, int N, int K) {
   return (p.tile || p.dgemm) && K % 4 == 0 && K <= kSplitThreads * 4 * kSplitV;
 }
 
+// Packed weight layout (lane_wbase): 16-byte unit d of the packed buffer is lane L = d % 64 of
+// group g = (d / 64) % G of tile t = d / (64 G): row 16 t + L % 16, bytes 64 g + 16 (L / 16) ..
+// +15 of that row, zero for the padding rows past N. Reads are 64-byte runs of 16 rows, writes
+// are contiguous.
+__global__ __launch_bounds__(kThreads) void pack_weights_kernel(const int8_t* __restrict__ w,
+                                                                int N, int K,
+                                                                u32x4* __restrict__ wp,
+                                                                size_t units) {
+  const int G = K / BK;
+  for (size_t d = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x; d < units;
+       d += static_cast<size_t>(gridDim.x) * kThreads) {
+    const int L = static_cast<int>(d & 63);
+    const size_t tg = d >> 6;
+    const int g = static_cast<int>(tg % G);
+    const size_t row = (tg / G) * 16 + (L & 15);
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (row < static_cast<size_t>(N))
+      v = *reinterpret_cast<const u32x4*>(w + row * K + g * BK + (L >> 4) * 16);
+    wp[d] = v;
+  }
+}
+
+hipError_t launch_pack_weights(const int8_t* w, int N, int K, int8_t* wp, hipStream_t st) {
+  const size_t units = static_cast<size_t>((N + 15) / 16) * 16 * K / 16;
+  const int grid = static_cast<int>(std::min<size_t>((units + kThreads - 1) / kThreads, 8192));
+  hipLaunchKernelGGL(pack_weights_kernel, dim3(grid), dim3(kThreads), 0, st, w, N, K,
+                     reinterpret_cast<u32x4*>(wp), units);
+  return hipGetLastError();
+}
+
+bool mfma_packed_ok(int M, int N, int K) { return M > 0 && N > 0 && K > 0; }
+
+// Either path's need: whether the GEMV serves a call also depends on the scales' alignment.
+size_t packed_workspace_bytes(int M, int N, int K, int gs) {
+  const size_t b = mfma_workspace_bytes(M, N, K);
+  if (!pgemv_ok(M, K, gs, nullptr)) return b;
+  const PgPlan p = pgemv_plan(M, N, K);
+  size_t g = kTicketBytes;
+  if (p.S > 1) g += align256(static_cast<size_t>(p.S) * M * N * sizeof(float));
+  return std::max(b, g);
+}
+
 hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
-                       int K, int gs, void* ws, hipStream_t st, Epi epi, const NormArgs* na) {
+                       int K, int gs, void* ws, hipStream_t st, Epi epi, const NormArgs* na,
+                       int pk) {
+  if (pk && pgemv_ok(M, K, gs, s)) {
+    if (epi.mode != kEpiNone || na) return hipErrorInvalidValue;
+    return launch_pgemv(x, w, s, y, ws, M, N, K, st);
+  }
   const Plan p = make_plan(M, N, K);
   if (epi.mode != kEpiNone && (p.tile || p.skinny)) return hipErrorInvalidValue;
   if (na && !mfma_norm_fused(M, N, K)) return hipErrorInvalidValue;
   if (p.dgemm) {
     switch (p.rt) {
-      case 1: return launch_dgemm<1>(x, w, s, y, ws, M, N, K, gs, p, st, epi, na);
-      case 2: return launch_dgemm<2>(x, w, s, y, ws, M, N, K, gs, p, st, epi, na);
-      case 3: return launch_dgemm<3>(x, w, s, y, ws, M, N, K, gs, p, st, epi, na);
-      default: return launch_dgemm<4>(x, w, s, y, ws, M, N, K, gs, p, st, epi, na);
+      case 1: return launch_dgemm<1>(x, w, s, y, ws, M, N, K, gs, p, st, epi, na, pk);
+      case 2: return launch_dgemm<2>(x, w, s, y, ws, M, N, K, gs, p, st, epi, na, pk);
+      case 3: return launch_dgemm<3>(x, w, s, y, ws, M, N, K, gs, p, st, epi, na, pk);
+      default: return launch_dgemm<4>(x, w, s, y, ws, M, N, K, gs, p, st, epi, na, pk);
     }
   }
   unsigned* tickets = static_cast<unsigned*>(ws);
@@ -1857,14 +2092,14 @@ hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y
   if (p.tile) {
     const int key = p.rt * 100 + p.tn * 10 + (p.tw >= 8 ? 8 : p.tw);
     switch (key) {
-      case 128: return launch_tile<1, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st, na);
-      case 144: return launch_tile<1, 4, 4>(x, w, s, y, ws, M, N, K, gs, p, st, na);
-      case 228: return launch_tile<2, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st, na);
-      case 244: return launch_tile<2, 4, 4>(x, w, s, y, ws, M, N, K, gs, p, st, na);
-      case 328: return launch_tile<3, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st, na);
-      case 342: return launch_tile<3, 4, 2>(x, w, s, y, ws, M, N, K, gs, p, st, na);
-      case 428: return launch_tile<4, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st, na);
-      case 442: return launch_tile<4, 4, 2>(x, w, s, y, ws, M, N, K, gs, p, st, na);
+      case 128: return launch_tile<1, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st, na, pk);
+      case 144: return launch_tile<1, 4, 4>(x, w, s, y, ws, M, N, K, gs, p, st, na, pk);
+      case 228: return launch_tile<2, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st, na, pk);
+      case 244: return launch_tile<2, 4, 4>(x, w, s, y, ws, M, N, K, gs, p, st, na, pk);
+      case 328: return launch_tile<3, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st, na, pk);
+      case 342: return launch_tile<3, 4, 2>(x, w, s, y, ws, M, N, K, gs, p, st, na, pk);
+      case 428: return launch_tile<4, 2, 8>(x, w, s, y, ws, M, N, K, gs, p, st, na, pk);
+      case 442: return launch_tile<4, 4, 2>(x, w, s, y, ws, M, N, K, gs, p, st, na, pk);
       default: return hipErrorInvalidValue;
     }
   }
@@ -1872,19 +2107,19 @@ hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y
     float* part = reinterpret_cast<float*>(base);
 #define SQ8_SKINNY(MR, MT16)                                                               \
   switch (p.kw) {                                                                          \
-    case 4: return launch_skinny16<MR, 4, 1, MT16>(x, w, s, y, part, tickets, M, N, K, gs, p, st); \
-    case 2: return launch_skinny16<MR, 2, 1, MT16>(x, w, s, y, part, tickets, M, N, K, gs, p, st); \
-    default: return launch_skinny16<MR, 1, 1, MT16>(x, w, s, y, part, tickets, M, N, K, gs, p, st); \
+    case 4: return launch_skinny16<MR, 4, 1, MT16>(x, w, s, y, part, tickets, M, N, K, gs, p, st, pk); \
+    case 2: return launch_skinny16<MR, 2, 1, MT16>(x, w, s, y, part, tickets, M, N, K, gs, p, st, pk); \
+    default: return launch_skinny16<MR, 1, 1, MT16>(x, w, s, y, part, tickets, M, N, K, gs, p, st, pk); \
   }
     if (M <= 4) {  // int8-limb MFMA kernel: one MFMA covers 4 tokens
-      if (p.kw == 4) return launch_skinny_i8<1, 4, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st);
-      if (p.kw == 2) return launch_skinny_i8<1, 2, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st);
-      return launch_skinny_i8<1, 1, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st);
+      if (p.kw == 4) return launch_skinny_i8<1, 4, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st, pk);
+      if (p.kw == 2) return launch_skinny_i8<1, 2, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st, pk);
+      return launch_skinny_i8<1, 1, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st, pk);
     }
     if (M <= 8 && p.kw == 4)
-      return launch_skinny16<8, 4, 1, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st);
+      return launch_skinny16<8, 4, 1, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st, pk);
     if (M <= 8 && p.kw == 2)
-      return launch_skinny16<8, 2, 1, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st);
+      return launch_skinny16<8, 2, 1, 1>(x, w, s, y, part, tickets, M, N, K, gs, p, st, pk);
     if (M <= 16) SQ8_SKINNY(16, 1);
     if (M <= 32) SQ8_SKINNY(32, 2);
     if (M <= 48) SQ8_SKINNY(48, 3);
@@ -1904,10 +2139,10 @@ hipError_t launch_mfma(const float* x, const int8_t* w, const float* s, float* y
   if (e != hipSuccess) return e;
   if (p.cfg == 1)
     e = p.gps == 1
-            ? launch_gemm<1, 4, 2, 2, 3>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st, epi)
-            : launch_gemm<2, 4, 1, 2, 2, 2>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st, epi);
+            ? launch_gemm<1, 4, 2, 2, 3>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st, epi, pk)
+            : launch_gemm<2, 4, 1, 2, 2, 2>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st, epi, pk);
   else
-    e = launch_gemm<2, 4, 2, 2, 3>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st, epi);
+    e = launch_gemm<2, 4, 2, 2, 3>(xh, xl, rsc, w, s, part, M, N, K, gs, p, st, epi, pk);
   if (e != hipSuccess || p.splits == 1) return e;
   const size_t count = static_cast<size_t>(M) * (epi.mode == kEpiSwiglu ? N / 2 : N);
   const int grid = static_cast<int>(std::min<size_t>((count + kThreads - 1) / kThreads, 4096));
