@@ -35,13 +35,33 @@ Third deviation: a victim cut back into its prompt resumes its prefill at min(it
 progress, the cut). The reference resumes at the cut (truncate_sequence, :320-327), which skips
 prompt positions never written when the prefill had not reached the cut.
 
-Not carried over: the content-hash prefix cache (scheduler.cpp:200-246), sentence-end tokens
-(random-init models have none) and timing statistics.
+Prefix cache (prefix_cache.cpp, admission at scheduler.cpp:200-246, recording at :483-487): a
+fresh request whose prompt starts with whole blocks another sequence has already prefilled mounts
+those physical blocks read-only at the front of its block table (reference counts keep them alive)
+and starts its prefill after them. Blocks are recorded when the owner's prefill completes; a
+lookup takes an entry only while its block is still referenced and still mounted at the recorded
+(row, index), so freed, recycled or truncated blocks are never shared.
+Deliberate deviations in the prefix cache:
+  - the key of block b is the whole token prefix [0, (b + 1) * block_size), compared exactly. The
+    reference keys each block by a 64-bit FNV-1a hash of that block's tokens alone, so block b can
+    match a block recorded after a different prefix, whose KV (a function of every earlier token)
+    differs; and it accepts hash collisions as matches;
+  - at most (prompt - 1) // block_size blocks are shared, so the block holding the prompt's last
+    position is private: this scheduler re-runs that token as the first decode row, and its KV
+    write must not land in a block other sequences read;
+  - an entry also records which allocation of the block it saw (a per-block counter bumped on
+    every allocation). The reference checks only that the block is referenced and mounted at the
+    recorded (row, index); after the owner finishes, the LIFO free list readily gives the same
+    block to a new sequence in the same row at the same index, and that block, holding the new
+    sequence's KV, would pass both checks.
+Sentence-end tokens (update_sequences, :681-690): a sequence whose last generated token is one of
+`stop_tokens` retires (the reference asks the model's tokenizer, is_sentence_ending). Timing
+statistics are not carried over.
 """
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from typing import Callable, List, Optional
+from typing import Callable, Dict, Iterable, List, Optional, Tuple
 
 WAITING, RUNNING, PREEMPTED, FINISHED = "waiting", "running", "preempted", "finished"
 
@@ -59,6 +79,8 @@ class BlockAllocator:
         self.free: List[int] = list(range(num_blocks - 1, -1, -1))
         self.ref = [0] * num_blocks
         self.tables = [[-1] * max_blocks_per_seq for _ in range(num_rows)]
+        self.row_used = [False] * num_rows  # a row may hold no blocks yet (allocate_blocks(0))
+        self.gen = [0] * num_blocks  # bumped on every allocation of a block
 
     def free_block_count(self) -> int:
         return len(self.free)
@@ -72,18 +94,35 @@ class BlockAllocator:
         b = self.free.pop()
         assert self.ref[b] == 0, f"block {b} in the free list with refcount {self.ref[b]}"
         self.ref[b] = 1
+        self.gen[b] += 1
         return b
 
     def allocate_blocks(self, n: int) -> int:
         """A free table row with n fresh blocks; -1 when rows or blocks run out."""
         if n > self.max_blocks_per_seq or n < 0 or len(self.free) < n:
             return -1
-        row = next((r for r in range(self.num_rows) if self.tables[r][0] == -1), -1)
+        row = next((r for r in range(self.num_rows) if not self.row_used[r]), -1)
         if row < 0:
             return -1
+        self.row_used[row] = True
         for i in range(n):
             self.tables[row][i] = self._take()
         return row
+
+    def reserve_shared_prefix(self, row: int, blocks: List[int]) -> bool:
+        """Mount `blocks` (already referenced elsewhere) at the front of `row`'s table, shifting
+        its own blocks right, and take a reference on each (block_allocator.cpp)."""
+        if row < 0 or row >= self.num_rows or not self.row_used[row]:
+            return False
+        used = self.num_used_blocks(row)
+        if used + len(blocks) > self.max_blocks_per_seq:
+            return False
+        own = self.tables[row][:used]
+        self.tables[row][:len(blocks) + used] = list(blocks) + own
+        for b in blocks:
+            assert self.ref[b] > 0, f"sharing block {b} with refcount 0"
+            self.ref[b] += 1
+        return True
 
     def append_blocks(self, row: int, n: int) -> int:
         """Grow a row by n blocks; returns the new block count or -1."""
@@ -111,9 +150,55 @@ class BlockAllocator:
 
     def free_all(self, row: int) -> None:
         self.free_blocks_from(row, 0)
+        if 0 <= row < self.num_rows:
+            self.row_used[row] = False
 
     def table_row(self, row: int) -> List[int]:
         return list(self.tables[row])
+
+
+class PrefixCache:
+    """Whole-block prompt prefixes whose KV is committed, for read-only sharing
+    (prefix_cache.cpp). Block b of a prompt is keyed by the prompt's tokens [0, (b + 1) *
+    block_size) (exact comparison); an entry names the (row, index, block, allocation) that held
+    it, and is valid only while that allocation of the block is alive and still mounted there."""
+
+    MAX_ENTRIES = 1 << 16  # a full flush beats unbounded growth (prefix_cache.cpp:47-53)
+
+    def __init__(self, block_size: int):
+        self.bs = block_size
+        self.map: Dict[Tuple[int, ...], List[Tuple[int, int, int, int]]] = {}
+
+    def lookup(self, prompt: List[int], alloc: BlockAllocator, max_blocks: int) -> List[int]:
+        """Physical blocks of the longest shareable whole-block prefix (at most max_blocks)."""
+        shared: List[int] = []
+        for b in range(min(len(prompt) // self.bs, max_blocks)):
+            found = -1
+            for row, idx, blk, gen in self.map.get(tuple(prompt[:(b + 1) * self.bs]), ()):
+                if alloc.ref[blk] > 0 and alloc.gen[blk] == gen and alloc.tables[row][idx] == blk:
+                    found = blk
+                    break
+            if found < 0:
+                break
+            shared.append(found)
+        return shared
+
+    def insert(self, prompt: List[int], alloc: BlockAllocator, row: int) -> None:
+        """Record the full prompt blocks of `row` (call when its prefill completes)."""
+        full = len(prompt) // self.bs
+        if full <= 0:
+            return
+        if len(self.map) >= self.MAX_ENTRIES:
+            self.map.clear()
+        for b in range(full):
+            entries = self.map.setdefault(tuple(prompt[:(b + 1) * self.bs]), [])
+            blk = alloc.tables[row][b]
+            entry = (row, b, blk, alloc.gen[blk])
+            if entry not in entries:
+                entries.append(entry)
+
+    def __len__(self) -> int:
+        return len(self.map)
 
 
 @dataclass
@@ -128,6 +213,7 @@ class Sequence:
     next_prefill: int = 0
     prefill_complete: bool = False
     finished: bool = False
+    shared_blocks: int = 0  # prompt blocks mounted from the prefix cache at admission
 
     @property
     def num_prompt(self) -> int:
@@ -148,7 +234,8 @@ Forward = Callable[[List[BatchRow], List[List[int]]], List[int]]
 
 class Scheduler:
     def __init__(self, forward: Forward, max_batch: int, max_seq_len: int,
-                 max_gen_len: int = 0, block_size: int = 16, num_blocks: Optional[int] = None):
+                 max_gen_len: int = 0, block_size: int = 16, num_blocks: Optional[int] = None,
+                 prefix_cache: bool = False, stop_tokens: Iterable[int] = ()):
         self.forward = forward
         self.max_batch, self.max_seq_len = max_batch, max_seq_len
         self.max_gen_len = max_gen_len if max_gen_len > 0 else max_seq_len
@@ -165,6 +252,9 @@ class Scheduler:
         self.steps = 0
         self.rows_run = 0
         self.preemptions = 0
+        self.prefix = PrefixCache(block_size) if prefix_cache else None
+        self.stop_tokens = frozenset(int(t) for t in stop_tokens)
+        self.shared_prefix_blocks = 0  # blocks mounted from the prefix cache, over the run
 
     @staticmethod
     def resolve_block_size(avg_prompt_len: float) -> int:
@@ -199,14 +289,29 @@ class Scheduler:
                 continue
             need = (seq.num_prompt + self.block_size - 1) // self.block_size
             self.waiting.pop(0)  # out of the queue before victims are pushed to its head
-            row = self.alloc.allocate_blocks(need)
-            if row < 0 and self._preempt_for(need, seq.id):
-                row = self.alloc.allocate_blocks(need)
+            shared = self._lookup(seq)
+            row = self.alloc.allocate_blocks(need - len(shared))
+            if row < 0 and self._preempt_for(need - len(shared), seq.id):
+                # eviction may have released the matched blocks: match again
+                shared = self._lookup(seq)
+                row = self.alloc.allocate_blocks(need - len(shared))
             if row < 0:
                 self.waiting.insert(0, seq)  # keeps its place: first in line
                 break
+            if shared:
+                assert self.alloc.reserve_shared_prefix(row, shared)
+                seq.next_prefill = len(shared) * self.block_size
+                seq.shared_blocks = len(shared)
+                self.shared_prefix_blocks += len(shared)
             seq.kv_row, seq.num_blocks, seq.state = row, need, RUNNING
             self.running.append(seq)
+
+    def _lookup(self, seq: Sequence) -> List[int]:
+        if self.prefix is None:
+            return []
+        # the block of the prompt's last position stays private (it is written again)
+        return self.prefix.lookup(seq.prompt_tokens, self.alloc,
+                                  (seq.num_prompt - 1) // self.block_size)
 
     def _preempt_for(self, need_blocks: int, skip_id: int, protect=frozenset()) -> bool:
         needed = need_blocks - self.alloc.free_block_count()
@@ -311,6 +416,8 @@ class Scheduler:
                 s.next_prefill += take
                 if s.next_prefill >= s.num_prompt:
                     s.prefill_complete = True
+                    if self.prefix is not None:  # the prompt's KV is written in this step
+                        self.prefix.insert(s.prompt_tokens, self.alloc, s.kv_row)
         return rows
 
     # ------------------------------------------------------------------ one step
@@ -331,7 +438,9 @@ class Scheduler:
     def _retire(self) -> None:
         keep = []
         for s in self.running:
-            if s.finished or len(s.generated_tokens) >= s.max_gen_len:
+            stop = (s.prefill_complete and s.generated_tokens and
+                    s.generated_tokens[-1] in self.stop_tokens)
+            if s.finished or stop or len(s.generated_tokens) >= s.max_gen_len:
                 s.finished, s.state = True, FINISHED
                 self.alloc.free_all(s.kv_row)
                 self.finished.append(s)

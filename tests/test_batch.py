@@ -309,3 +309,42 @@ def test_continuous_batching_long_rows_split_kv(dev, tmp_path):
     done = s.run(max_steps=5000)
     assert model.graph_replays > 0
     assert [q.generated_tokens for q in done] == ref
+
+
+@pytest.mark.gpu
+def test_prefix_cache_on_the_gpu_matches_oracle(dev, tmp_path):
+    """Prefix cache with the HIP batch model: later requests mount the KV blocks of a running
+    sequence that share their whole-block prompt prefix (block 8) and start their prefill after
+    them; their greedy tokens equal the float64 oracle decoding each prompt alone. A stop token
+    (the first request's 3rd token) retires sequences early."""
+    sched = importlib.import_module("llm_steadyinfer_amd.scheduler")
+    bm = importlib.import_module("llm_steadyinfer_amd.batch_model")
+    dec = importlib.import_module("llm_steadyinfer_amd.decoder")
+    path = mf.write_random(tmp_path / "m.bin", TINY, 64, seed=13, w_std=0.2)
+    rng = np.random.default_rng(13)
+    base = rng.integers(0, TINY.vocab, 24).tolist()
+    first = base + [1, 2]
+    later = [base + [3], base[:16] + [4, 5, 6], base[:8] + rng.integers(0, TINY.vocab, 9).tolist(),
+             rng.integers(0, TINY.vocab, 10).tolist()]
+    n_new, max_seq, bs = 12, 64, 8
+    oracle = lambda p: do.DecodeModel(mf.ModelFile(path), max_seq=max_seq).generate(p, n_new)[0]
+    ref = [oracle(p) for p in [first] + later]
+    stop = ref[0][2]
+    D = dec.Int8Decoder.from_file(path, max_seq=max_seq, device=dev)
+    s = sched.Scheduler(None, max_batch=4, max_seq_len=max_seq, max_gen_len=n_new,
+                        block_size=bs, prefix_cache=True, stop_tokens=[stop])
+    model = bm.PagedBatchModel.from_decoder(D, max_rows=4, max_seq_len=max_seq,
+                                            num_blocks=s.alloc.num_blocks, block_size=bs)
+    s.forward = model.forward
+    assert s.add_request(first) >= 0
+    while not (s.running and s.running[0].prefill_complete):
+        s.step()
+    for p in later:
+        assert s.add_request(p) >= 0
+    done = s.run(max_steps=5000)
+    print("shared blocks", s.shared_prefix_blocks, "steps", s.steps)
+    assert s.shared_prefix_blocks >= 3 + 2 + 1
+    for q, r in zip(done, ref):
+        cut = next((k + 1 for k, t in enumerate(r) if t == stop), len(r))
+        assert q.generated_tokens == r[:cut], q.id
+    assert len(done[0].generated_tokens) == 3

@@ -155,3 +155,190 @@ def test_resolve_block_size():
     assert Scheduler.resolve_block_size(10) == 8
     assert Scheduler.resolve_block_size(200) == 16
     assert Scheduler.resolve_block_size(2000) == 32
+
+
+# ----------------------------------------------------------------------------- prefix cache, stop
+class ChainModel(FakeModel):
+    """Like FakeModel, but the value stored at position p depends on the value at p - 1 read back
+    through the row's block table (as a transformer's KV depends on every earlier token), and no
+    row may write into a block another row also references (shared prefix blocks are read-only).
+    Rows of one sequence in a step come in position order, so p - 1 is always written first."""
+
+    def __init__(self, block_size):
+        super().__init__(block_size)
+        self.alloc = None
+
+    def __call__(self, rows, tables):
+        self.calls.append(rows)
+        for r, t in zip(rows, tables):
+            blk = t[r.position // self.bs]
+            assert blk >= 0, "position beyond the row's blocks"
+            assert self.alloc.ref[blk] == 1, f"write into shared block {blk}"
+            prev = self.kv[(t[(r.position - 1) // self.bs], (r.position - 1) % self.bs)] \
+                if r.position > 0 else 17
+            self.kv[(blk, r.position % self.bs)] = (prev * 1000033 + r.token * 31 + r.position) \
+                % 998244353
+        return [self.kv[(t[r.position // self.bs], r.position % self.bs)] % 5000
+                for r, t in zip(rows, tables) if r.is_decode]
+
+
+def run_chain(prompts, max_batch, max_gen, block_size, num_blocks=None, prefix=True, stop=(),
+              max_seq=None, stagger=False):
+    """Run the prompts; with stagger the first request runs alone until its prefill completes
+    and the rest arrive then (entries exist only once an owner's prefill is done, and stay valid
+    while the owner runs)."""
+    fake = ChainModel(block_size)
+    max_seq = max_seq or max(len(p) for p in prompts) + max_gen
+    s = Scheduler(fake, max_batch=max_batch, max_seq_len=max_seq, max_gen_len=max_gen,
+                  block_size=block_size, num_blocks=num_blocks, prefix_cache=prefix,
+                  stop_tokens=stop)
+    fake.alloc = s.alloc
+    rest = prompts
+    if stagger:
+        assert s.add_request(prompts[0]) >= 0
+        while not s.running or not s.running[0].prefill_complete:
+            s.step()
+        rest = prompts[1:]
+    assert all(s.add_request(p) >= 0 for p in rest)
+    done = s.run(max_steps=20000)
+    return {q.id: q.generated_tokens for q in done}, s
+
+
+def chain_reference(prompts, max_gen, block_size):
+    return {i: run_chain([p], 1, max_gen, block_size, prefix=False)[0][0]
+            for i, p in enumerate(prompts)}
+
+
+_rng = np.random.default_rng(99)
+BASE = [int(t) for t in _rng.integers(0, 5000, 40)]
+OTHER = [int(t) for t in _rng.integers(0, 5000, 40)]
+SHARED_PROMPTS = [
+    BASE + [1, 2, 3],            # shares BASE's whole blocks with the next ones
+    BASE + [4, 5, 6, 7, 8],
+    BASE[:32],                   # a prefix exactly two blocks long (last block stays private)
+    BASE[:16] + OTHER[16:40],    # block 1 differs after a shared block 0
+    OTHER[:16] + BASE[16:40],    # block 1 equals BASE's block 1 after a different block 0
+    BASE + [1, 2, 3],            # an exact repeat
+    [9] * 5,
+    BASE[:33],
+]
+
+
+@pytest.mark.parametrize("max_batch", [2, 3, 8])
+def test_prefix_cache_tokens_equal_unshared(max_batch):
+    ref = chain_reference(SHARED_PROMPTS, 30, 16)
+    got, s = run_chain(SHARED_PROMPTS, max_batch, 30, 16, stagger=True)
+    assert got == ref
+    assert s.shared_prefix_blocks > 0
+    assert s.alloc.free_block_count() == s.alloc.num_blocks and all(c == 0 for c in s.alloc.ref)
+    assert len(s.prefix) > 0
+
+
+def test_prefix_cache_skips_prefill_of_shared_blocks():
+    """The rows run are fewer by exactly the shared positions, and the tokens are unchanged."""
+    plain, s0 = run_chain(SHARED_PROMPTS, 8, 30, 16, prefix=False, stagger=True)
+    shared, s1 = run_chain(SHARED_PROMPTS, 8, 30, 16, stagger=True)
+    assert plain == shared
+    # After the first prompt's prefill: BASE + [4..8] and the repeat share 2 blocks each,
+    # BASE[:32] 1 (its last block stays private), BASE[:16] + OTHER 1, BASE[:33] 2,
+    # OTHER[:16] + BASE[16:] and [9] * 5 none.
+    assert s1.shared_prefix_blocks == 2 + 2 + 1 + 1 + 2
+    assert s0.rows_run - s1.rows_run == 16 * s1.shared_prefix_blocks
+
+
+def test_prefix_cache_is_off_by_default():
+    _, s = run_chain(SHARED_PROMPTS, 8, 30, 16, prefix=False, stagger=True)
+    assert s.prefix is None and s.shared_prefix_blocks == 0
+
+
+def run_script(script, max_batch, max_gen, block_size, prefix=True):
+    """Requests arrive in phases: each phase's prompts are added, then the scheduler steps until
+    `until(s)` holds (a callable on the scheduler)."""
+    fake = ChainModel(block_size)
+    max_seq = max(len(p) for ps, _ in script for p in ps) + max_gen
+    s = Scheduler(fake, max_batch=max_batch, max_seq_len=max_seq, max_gen_len=max_gen,
+                  block_size=block_size, prefix_cache=prefix)
+    fake.alloc = s.alloc
+    for prompts, until in script:
+        for p in prompts:
+            assert s.add_request(p) >= 0
+        while not until(s):
+            s.step()
+    s.run(max_steps=20000)
+    return {q.id: q.generated_tokens for q in s.finished}, s
+
+
+def prefilled(n):
+    """Until the first n requests have completed their prefill (or finished)."""
+    return lambda s: sum(1 for q in s.running + s.finished if q.prefill_complete or q.finished) \
+        >= n
+
+
+def test_prefix_cache_key_is_the_whole_prefix():
+    """Owners X + Y and W + Z are both alive when X + Z arrives. Block 0 (X) matches the first
+    owner; block 1 has Z's tokens, as the second owner's block 1 does, but that block's KV was
+    computed after W: keyed by the whole prefix it does not match (keyed by the block's own
+    tokens it would, and the chain model's tokens would change)."""
+    X, Y, W, Z = (BASE[:16], BASE[16:32], OTHER[:16], OTHER[16:32])
+    owners = [X + Y + [1, 2], W + Z + [3, 4]]
+    late = [X + Z + [5, 6]]
+    got, s = run_script([(owners, prefilled(2)), (late, lambda s: True)], 3, 30, 16)
+    ref = chain_reference(owners + late, 30, 16)
+    assert got == ref
+    assert s.shared_prefix_blocks == 1  # only X
+
+
+def test_prefix_cache_rejects_reallocated_block():
+    """X = X0 + X1 + [1] and O = X0 + (200 tokens) run; X finishes holding 3 blocks and frees
+    them. Y (33 tokens) takes X's row and, from the LIFO free list, X's blocks in reverse order,
+    so X's block 1 is mounted again at index 1 of the same row, now holding Y's KV. C = X0 + X1
+    + [...] then finds block 0 in O (valid) and, for block 1, X's entry: the block is referenced
+    and mounted at the recorded (row, index), but it is another allocation of it. The
+    per-allocation counter rejects it (without it the chain model's tokens change)."""
+    X0, X1 = BASE[:16], BASE[16:32]
+    long_tail = [int(t) for t in np.random.default_rng(5).integers(0, 5000, 200)]
+    X, O, Y, C = X0 + X1 + [1], X0 + long_tail, OTHER[:33], X0 + X1 + [5, 6]
+    x_done = lambda s: any(q.id == 0 for q in s.finished)
+    got, s = run_script([([X, O], x_done), ([Y], prefilled(3)), ([C], lambda s: True)], 4, 12,
+                        16)
+    assert got == chain_reference([X, O, Y, C], 12, 16)
+    assert s.shared_prefix_blocks == 1  # block 0 from O only
+
+
+@pytest.mark.parametrize("num_blocks", [14, 16, 18, 20])
+def test_prefix_cache_survives_preemption(num_blocks):
+    """Pools too small for the running set: sequences holding shared blocks are cut back and
+    resumed (or finished early when they cannot grow); every sequence's tokens are a prefix of
+    its unshared run and every reference is returned."""
+    ref = chain_reference(SHARED_PROMPTS, 24, 8)
+    got, s = run_chain(SHARED_PROMPTS, 4, 24, 8, num_blocks=num_blocks, stagger=True)
+    assert s.preemptions > 0 and s.shared_prefix_blocks > 0
+    for i, toks in got.items():
+        assert toks == ref[i][:len(toks)], i
+    assert s.alloc.free_block_count() == num_blocks and all(c == 0 for c in s.alloc.ref)
+
+
+def test_stop_tokens_retire_sequences():
+    ref = chain_reference(PROMPTS, 12, 4)
+    stop = {ref[0][3], ref[5][6]}
+    got, s = run_chain(PROMPTS, 4, 12, 4, prefix=False, stop=stop)
+    for i, toks in got.items():
+        cut = next((k + 1 for k, t in enumerate(ref[i]) if t in stop), len(ref[i]))
+        assert toks == ref[i][:cut], i
+    assert len(got[0]) == 4
+
+
+def test_block_allocator_shared_prefix_rows():
+    a = BlockAllocator(num_blocks=6, num_rows=3, max_blocks_per_seq=4, block_size=4)
+    r0 = a.allocate_blocks(3)                  # blocks 0, 1, 2
+    r1 = a.allocate_blocks(0)                  # a row with no blocks yet is still taken
+    assert (r0, r1) == (0, 1) and a.allocate_blocks(1) == 2
+    assert a.append_blocks(r1, 1) == 1          # its own block first ...
+    assert a.reserve_shared_prefix(r1, [0, 1])  # ... then the shared ones mounted in front
+    assert a.table_row(r1) == [0, 1, 4, -1] and a.ref[0] == a.ref[1] == 2
+    assert not a.reserve_shared_prefix(r1, [0, 1, 2])  # would overflow the row
+    a.free_all(r0)
+    assert a.ref[0] == a.ref[1] == 1 and a.ref[2] == 0 and 2 in a.free
+    a.free_all(r1)
+    a.free_all(2)
+    assert a.free_block_count() == 6 and all(c == 0 for c in a.ref)
