@@ -92,8 +92,10 @@ class Call:
     def __init__(self, sq8, x, q, s, y, stream, ws):
         M, K = x.shape
         N = q.shape[0]
-        self.fn = sq8.lib().sq8_matmul
-        wsb = sq8.workspace_bytes(M, N, K, GS)
+        packed = isinstance(q, sq8.PackedWeight)
+        self.fn = sq8.lib().sq8_matmul_packed if packed else sq8.lib().sq8_matmul
+        wsb = (int(sq8.lib().sq8_packed_workspace_bytes(M, N, K, GS)) if packed
+               else sq8.workspace_bytes(M, N, K, GS))
         ws_ptr, ws_n = ws.get(wsb)
         self.args = (x.data_ptr(), q.data_ptr(), s.data_ptr(), y.data_ptr(), M, N, K, GS,
                      ws_ptr or None, ws_n, stream.cuda_stream)
@@ -104,7 +106,7 @@ class Call:
     def __call__(self):
         rc = self.fn(*self.args)
         if rc != 0:
-            raise RuntimeError(f"sq8_matmul failed with status {rc}")
+            raise RuntimeError(f"sq8 matmul failed with status {rc}")
 
 
 def cpu_baseline(torch, weights, budget_s=10.0):
@@ -283,7 +285,7 @@ def copy_ceiling(torch, dev, shapes):
 
 
 def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed: int = 0,
-              sigma: float = 0.8):
+              sigma: float = 0.8, packed: bool = False):
     """Config 5: continuous batching of n_seqs requests on the Llama-3-8B-shaped INT8 model (the
     step's random-init projections, plus a random embedding and unit norms). Prompt lengths are
     lognormal with median 200 (sigma 0.8, clipped to 16..2048), uniform random token ids,
@@ -313,7 +315,8 @@ def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed:
     s = sch.Scheduler(None, max_batch=64, max_seq_len=max_seq, max_gen_len=n_new,
                       block_size=block)
     model = bm.PagedBatchModel(cfg, w, GS, max_rows=64, max_seq_len=max_seq,
-                               num_blocks=s.alloc.num_blocks, block_size=block, device=dev)
+                               num_blocks=s.alloc.num_blocks, block_size=block, device=dev,
+                               packed=packed)
     # Decode-step graphs for every row count, captured at start-up (not timed).
     capture_s = model.capture_decode_graphs()
     s.forward = model.forward
@@ -334,7 +337,8 @@ def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed:
     return {"workload": f"config 5: Llama-3-8B-shaped random-init INT8 model, {n_seqs} sequences, "
                         f"lognormal prompts (median 200, sigma {sigma}, clipped 16..2048; "
                         f"mean {lens.mean():.0f}, max {int(lens.max())}), {n_new} greedy tokens "
-                        f"each, paged KV block {block}, max_batch 64",
+                        f"each, paged KV block {block}, max_batch 64" +
+                        (", packed weights" if packed else ""),
             "output_tokens_per_s": round(gen_tokens / wall, 1),
             "total_tokens_per_s": round((gen_tokens + prompt_tokens) / wall, 1),
             "wall_s": round(wall, 3), "generated_tokens": gen_tokens,
@@ -352,6 +356,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--packed", action="store_true",
+                    help="also time the 1-64-row sweep and config 5 on packed weights "
+                         "(sq8_pack_weights)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-batch", action="store_true", help="skip config 5 (continuous batching)")
@@ -582,11 +589,38 @@ def main():
         decode = decode_run(torch)
         print(f"# decode done: {decode['tokens_per_s']} tokens/s", file=sys.stderr, flush=True)
 
+    # The same 1-64-row shapes on packed weights (one repack per layer's weight).
+    sweep_packed = []
+    if args.packed and not args.no_sweep:
+        pw = {p: [(sq8.pack_weights(q), s_) for q, s_ in weights[p]] for p in PROJ}
+        for M in (1, 8, 32, 64):
+            for p, (N, K) in PROJ.items():
+                x, y = xbuf(M, K), torch.empty((M, N), device=dev)
+                cs = [Call(sq8, x, *pw[p][l], y, stream, ws) for l in range(LAYERS)]
+                cs[0]()
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(stream)
+                for c in cs:
+                    c()
+                b.record(stream)
+                torch.cuda.synchronize()
+                us = a.elapsed_time(b) * 1e3 / LAYERS
+                sweep_packed.append({"proj": p, "M": M, "N": N, "K": K, "us": round(us, 2),
+                                     "GB/s": round(cs[0].bytes / us / 1e3, 1)})
+                del x, y, cs
+        del pw
+        print("# packed sweep done", file=sys.stderr, flush=True)
+
     batch = None
     if not args.no_batch:
         batch = batch_run(torch, weights, lm_head)
         print(f"# batch done: {batch['output_tokens_per_s']} output tokens/s", file=sys.stderr,
               flush=True)
+    batch_packed = None
+    if args.packed and not args.no_batch:
+        batch_packed = batch_run(torch, weights, lm_head, packed=True)
+        print(f"# packed batch done: {batch_packed['output_tokens_per_s']} output tokens/s",
+              file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu:
@@ -610,11 +644,13 @@ def main():
         "decode": decode,
         "batch_output_tokens_per_s": batch["output_tokens_per_s"] if batch else None,
         "batch": batch,
+        "batch_packed": batch_packed,
         "step_algo_bytes": step_bytes,
         "roofline": roofline,
         "prefill_roofline": prefill,
         "cpu_baseline": cpu,
         "sweep": sweep,
+        "sweep_packed": sweep_packed or None,
     }
     print(json.dumps(out))
 

@@ -25,6 +25,10 @@ decode-only steps at that B replay it (one launch instead of ~15 per layer), the
 reference captures its decode steps (src/source/model/model.cpp:189-238). The matmul workspace is
 sized for every row count up front, so no later step can move a buffer a graph points to. The KV pool is [layers][num_blocks][block_size][kv_dim] fp32 for keys
 and for values (KVManager's paged layout, src/source/scheduler/kv_manager.cpp).
+
+With packed=True the projections are repacked once at start-up into the matrix-core kernels'
+load order (sq8_pack_weights: each 16-row tile's 64-wide groups as contiguous 1 KiB blocks) and
+every matmul takes the _packed entry points; the model then holds only the packed copies.
 """
 from __future__ import annotations
 
@@ -34,7 +38,7 @@ import numpy as np
 
 from . import (SQ8_EPI_NONE, SQ8_EPI_RESIDUAL, SQ8_EPI_SWIGLU, Workspace, add_rmsnorm,
                argmax_rows, embedding, epilogue_fused, lib, matmul, matmul_epilogue,
-               matmul_rmsnorm_rows,
+               matmul_rmsnorm_rows, pack_weights,
                paged_attention, paged_attention_workspace_bytes, paged_rope_kv, rmsnorm,
                rope_tables, swiglu_rows)
 
@@ -44,9 +48,15 @@ EPS = 1e-6
 class PagedBatchModel:
     def __init__(self, cfg, weights: dict, group_size: int, max_rows: int, max_seq_len: int,
                  num_blocks: int, block_size: int, device="cuda", use_graphs: bool = True,
-                 split_kv: bool = True, fuse_norm: bool = True):
+                 split_kv: bool = True, fuse_norm: bool = True, packed: bool = False):
         import torch
         self.torch = torch
+        self.packed = packed
+        if packed:  # one repack per projection at start-up; the model keeps only these copies
+            weights = dict(weights)
+            for key in ("qkv", "o", "gu", "down"):
+                weights[key] = [(pack_weights(q), s) for q, s in weights[key]]
+            weights["cls"] = (pack_weights(weights["cls"][0]), weights["cls"][1])
         self.cfg, self.w, self.gs = cfg, weights, group_size
         self.max_rows, self.block_size = max_rows, block_size
         self.max_blocks_per_seq = (max_seq_len + block_size - 1) // block_size
@@ -84,6 +94,13 @@ class PagedBatchModel:
         for B in range(1, R + 1):
             for (N, K) in ((d + 2 * kv, d), (d, d), (2 * h, d), (d, h), (cfg.vocab, d)):
                 for epi in (SQ8_EPI_NONE, SQ8_EPI_RESIDUAL, SQ8_EPI_SWIGLU):
+                    if packed:
+                        need = max(need, int(lib().sq8_epilogue_packed_workspace_bytes(
+                            B, N, K, group_size, epi)))
+                        if epi != SQ8_EPI_RESIDUAL:
+                            need = max(need, int(lib().sq8_rmsnorm_rows_packed_workspace_bytes(
+                                B, N, K, group_size, epi)))
+                        continue
                     need = max(need, int(lib().sq8_epilogue_workspace_bytes(B, N, K, group_size,
                                                                             epi)))
                     if epi != SQ8_EPI_RESIDUAL:
@@ -99,10 +116,12 @@ class PagedBatchModel:
     @classmethod
     def from_decoder(cls, dec, max_rows: int, max_seq_len: int, num_blocks: int,
                      block_size: int, use_graphs: bool = True, split_kv: bool = True,
-                     fuse_norm: bool = True) -> "PagedBatchModel":
-        """Share the fused weights of an Int8Decoder (model file or random init)."""
+                     fuse_norm: bool = True, packed: bool = False) -> "PagedBatchModel":
+        """Share the fused weights of an Int8Decoder (model file or random init); with packed
+        the model holds packed copies of the projections instead (sq8_pack_weights)."""
         return cls(dec.cfg, dec.w, dec.gs, max_rows, max_seq_len, num_blocks, block_size,
-                   dec.device, use_graphs=use_graphs, split_kv=split_kv, fuse_norm=fuse_norm)
+                   dec.device, use_graphs=use_graphs, split_kv=split_kv, fuse_norm=fuse_norm,
+                   packed=packed)
 
     def kv_bytes_per_position(self) -> int:
         return 2 * 4 * self.cfg.layer_num * self.cfg.kv_dim
@@ -138,8 +157,9 @@ class PagedBatchModel:
         if B not in self._fuse:
             cfg, gs = self.cfg, self.gs
             d, h = cfg.dim, cfg.hidden_dim
-            self._fuse[B] = (epilogue_fused(B, d, d, gs), epilogue_fused(B, 2 * h, d, gs),
-                             epilogue_fused(B, d, h, gs))
+            pk = self.packed
+            self._fuse[B] = (epilogue_fused(B, d, d, gs, pk), epilogue_fused(B, 2 * h, d, gs, pk),
+                             epilogue_fused(B, d, h, gs, pk))
         return self._fuse[B]
 
     def forward(self, rows, tables: List[List[int]]) -> List[int]:

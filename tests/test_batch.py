@@ -242,15 +242,17 @@ def test_swiglu_and_argmax_rows(sq8, dev):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("max_batch,block_size,num_blocks,graphs", [
-    (4, 4, None, True), (4, 4, 20, True), (4, 4, 24, True), (8, 8, None, True),
-    (96, 8, None, True), (8, 8, None, False)])
-def test_continuous_batching_matches_oracle(dev, tmp_path, max_batch, block_size, num_blocks,
-                                            graphs):
+@pytest.mark.parametrize("max_batch,block_size,num_blocks,graphs,packed", [
+    (4, 4, None, True, False), (4, 4, 20, True, False), (4, 4, 24, True, False),
+    (8, 8, None, True, False), (96, 8, None, True, False), (8, 8, None, False, False),
+    (4, 4, 24, True, True), (96, 8, None, True, True)])
+def test_continuous_batching_matches_oracle(sq8, dev, tmp_path, max_batch, block_size,
+                                            num_blocks, graphs, packed):
     """Six prompts (1..40 tokens) scheduled with chunked prefill mixed into decode steps (and,
     with a 20- or 24-block pool, preemption and recompute): every sequence's greedy tokens equal the
     float64 oracle decoding it alone. Decode-only steps replay per-row-count HIP graphs between
-    eager prefill steps (and run eagerly in the graphs=False case)."""
+    eager prefill steps (and run eagerly in the graphs=False case). With packed the model holds
+    packed weights (sq8_pack_weights) and every matmul takes the _packed entry points."""
     sched = importlib.import_module("llm_steadyinfer_amd.scheduler")
     bm = importlib.import_module("llm_steadyinfer_amd.batch_model")
     dec = importlib.import_module("llm_steadyinfer_amd.decoder")
@@ -265,7 +267,7 @@ def test_continuous_batching_matches_oracle(dev, tmp_path, max_batch, block_size
                         block_size=block_size, num_blocks=num_blocks)
     model = bm.PagedBatchModel.from_decoder(D, max_rows=max_batch, max_seq_len=max_seq,
                                             num_blocks=s.alloc.num_blocks, block_size=block_size,
-                                            use_graphs=graphs)
+                                            use_graphs=graphs, packed=packed)
     s.forward = model.forward
     for p in prompts:
         assert s.add_request(p) >= 0
@@ -278,6 +280,8 @@ def test_continuous_batching_matches_oracle(dev, tmp_path, max_batch, block_size
         assert s.preemptions > 0
     if max_batch > 64:  # the 88 prompt tokens start as one step: the fused-epilogue GEMM path
         assert model.fused(88) == (True, True, True)
+    if packed:
+        assert all(isinstance(q, sq8.PackedWeight) for q, _ in model.w["qkv"])
     assert got == ref
 
 
