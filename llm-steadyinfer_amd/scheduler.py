@@ -46,9 +46,10 @@ Deliberate deviations in the prefix cache:
     reference keys each block by a 64-bit FNV-1a hash of that block's tokens alone, so block b can
     match a block recorded after a different prefix, whose KV (a function of every earlier token)
     differs; and it accepts hash collisions as matches;
-  - at most (prompt - 1) // block_size blocks are shared, so the block holding the prompt's last
-    position is private: this scheduler re-runs that token as the first decode row, and its KV
-    write must not land in a block other sequences read;
+  - at most (prompt - 1) // block_size blocks are shared, and an owner records only that many,
+    so the block holding a prompt's last position is private on both sides: this scheduler
+    re-runs that token as the first decode row, and its KV write must not land in a block other
+    sequences read;
   - an entry also records which allocation of the block it saw (a per-block counter bumped on
     every allocation). The reference checks only that the block is referenced and mounted at the
     recorded (row, index); after the owner finishes, the LIFO free list readily gives the same
@@ -184,8 +185,10 @@ class PrefixCache:
         return shared
 
     def insert(self, prompt: List[int], alloc: BlockAllocator, row: int) -> None:
-        """Record the full prompt blocks of `row` (call when its prefill completes)."""
-        full = len(prompt) // self.bs
+        """Record the prompt blocks of `row` before the one holding the prompt's last position
+        (call when its prefill completes): the owner re-runs that position as its first decode
+        row, so that block is written again and must stay private."""
+        full = (len(prompt) - 1) // self.bs
         if full <= 0:
             return
         if len(self.map) >= self.MAX_ENTRIES:

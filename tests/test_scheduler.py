@@ -342,3 +342,15 @@ def test_block_allocator_shared_prefix_rows():
     a.free_all(r1)
     a.free_all(2)
     assert a.free_block_count() == 6 and all(c == 0 for c in a.ref)
+
+
+def test_prefix_cache_never_shares_the_owners_last_prompt_block():
+    """An owner whose prompt fills exactly two blocks re-runs its last prompt token as its first
+    decode row, writing position 31 of block 1 again. A request admitted in that same step must
+    not mount block 1 (the chain model asserts every written block is private), only block 0."""
+    owner = BASE[:32]
+    late = BASE[:32] + [7, 8, 9]
+    prefill_done = lambda s: any(q.prefill_complete for q in s.running)
+    got, s = run_script([([owner], prefill_done), ([late], lambda s: True)], 2, 12, 16)
+    assert got == chain_reference([owner, late], 12, 16)
+    assert s.shared_prefix_blocks == 1
