@@ -9,6 +9,8 @@ from __future__ import annotations
 import ctypes
 from pathlib import Path
 
+import numpy as np
+
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "libsq8.so"
 
@@ -216,6 +218,42 @@ def pack_weights(w, stream=None) -> PackedWeight:
     return PackedWeight(data, N, K)
 
 
+def _check_matmul(x, w, scales, y, group_size: int, out_cols: int, extra=()):
+    """The shape, dtype and placement checks of MatmulLayer::check (src/source/op/matmul.cpp:
+    19-77), made before anything is launched: the C ABI takes plain pointers and cannot see a
+    buffer's size, so a mismatch here would become an out-of-bounds access on the GPU.
+    x fp32 [M][K]; w int8 [N][K] (row-major or PackedWeight); scales fp32 [N*K/group_size];
+    y fp32 [M][out_cols]; extra: (name, tensor, shape) triples (fp32) checked the same way."""
+    import torch
+    M, K = x.shape
+    N = w.shape[0]
+    if tuple(w.shape) != (N, K):
+        raise ValueError(f"weight shape {tuple(w.shape)} does not match input width {K}")
+    if group_size <= 0 or (N * K) % group_size != 0:
+        raise ValueError(f"group size {group_size} does not divide the {N}x{K} weight")
+    wdt = w.data.dtype if isinstance(w, PackedWeight) else w.dtype
+    checks = [("input", x, torch.float32, (M, K)), ("weight", None, wdt, None),
+              ("scales", scales, torch.float32, (N * K // group_size,)),
+              ("output", y, torch.float32, (M, out_cols))]
+    checks += [(name, t, torch.float32, shape) for name, t, shape in extra]
+    if wdt != torch.int8:
+        raise ValueError(f"weight dtype {wdt}, expected torch.int8")
+    for name, t, dt, shape in checks:
+        if t is None:
+            continue
+        if t.dtype != dt:
+            raise ValueError(f"{name} dtype {t.dtype}, expected {dt}")
+        if t.numel() != int(np.prod(shape)):
+            raise ValueError(f"{name} holds {t.numel()} values, expected {shape}")
+        if not t.is_contiguous():
+            raise ValueError("sq8 tensors must be contiguous")
+    devs = {str(t.device) for t in (x, w, scales, y) + tuple(t for _, t, _ in extra)}
+    if len(devs) != 1:
+        raise ValueError(f"operands on different devices: {sorted(devs)}")
+    if x.device.type != "cuda":
+        raise ValueError(f"operands on {x.device}, expected a GPU")
+
+
 def matmul(x, w, scales, y=None, group_size: int = 64, workspace: Workspace | None = None,
            stream=None):
     """y[M,N] = x[M,K] @ dequant(w[N,K], scales).T on the current torch stream.
@@ -228,9 +266,7 @@ def matmul(x, w, scales, y=None, group_size: int = 64, workspace: Workspace | No
     N = w.shape[0]
     if y is None:
         y = torch.empty((M, N), dtype=torch.float32, device=x.device)
-    for t in (x2, w, scales, y):
-        if not t.is_contiguous():
-            raise ValueError("sq8 tensors must be contiguous")
+    _check_matmul(x2, w, scales, y, group_size, N)
     if stream is None:
         stream = torch.cuda.current_stream(x.device)
     if workspace is None:
@@ -264,9 +300,9 @@ def matmul_epilogue(x, w, scales, y, epilogue: int, residual=None, group_size: i
     import torch
     M, K = x.shape
     N = w.shape[0]
-    for t in (x, w, scales, y) + ((residual,) if residual is not None else ()):
-        if not t.is_contiguous():
-            raise ValueError("sq8 tensors must be contiguous")
+    out_cols = N // 2 if epilogue == SQ8_EPI_SWIGLU else N
+    extra = () if residual is None else (("residual", residual, (M, out_cols)),)
+    _check_matmul(x, w, scales, y, group_size, out_cols, extra)
     if stream is None:
         stream = torch.cuda.current_stream(x.device)
     if workspace is None:
@@ -296,9 +332,8 @@ def matmul_rmsnorm_rows(x, res, norm_w, eps: float, w, scales, y, epilogue: int 
     import torch
     M, K = x.shape
     N = w.shape[0]
-    for t in (x, w, scales, y, norm_w) + ((res,) if res is not None else ()):
-        if not t.is_contiguous():
-            raise ValueError("sq8 tensors must be contiguous")
+    extra = (("norm weight", norm_w, (K,)),) + (() if res is None else (("residual", res, (M, K)),))
+    _check_matmul(x, w, scales, y, group_size, N // 2 if epilogue == SQ8_EPI_SWIGLU else N, extra)
     if stream is None:
         stream = torch.cuda.current_stream(x.device)
     if workspace is None:
