@@ -7,9 +7,8 @@ only). There is no CPU fallback: if the HIP library is missing, ``lib()`` raises
 from __future__ import annotations
 
 import ctypes
+import math
 from pathlib import Path
-
-import numpy as np
 
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "libsq8.so"
@@ -232,27 +231,24 @@ def _check_matmul(x, w, scales, y, group_size: int, out_cols: int, extra=()):
     if group_size <= 0 or (N * K) % group_size != 0:
         raise ValueError(f"group size {group_size} does not divide the {N}x{K} weight")
     wdt = w.data.dtype if isinstance(w, PackedWeight) else w.dtype
-    checks = [("input", x, torch.float32, (M, K)), ("weight", None, wdt, None),
-              ("scales", scales, torch.float32, (N * K // group_size,)),
-              ("output", y, torch.float32, (M, out_cols))]
-    checks += [(name, t, torch.float32, shape) for name, t, shape in extra]
     if wdt != torch.int8:
         raise ValueError(f"weight dtype {wdt}, expected torch.int8")
-    for name, t, dt, shape in checks:
-        if t is None:
-            continue
-        if t.dtype != dt:
-            raise ValueError(f"{name} dtype {t.dtype}, expected {dt}")
-        if t.numel() != int(np.prod(shape)):
-            raise ValueError(f"{name} holds {t.numel()} values, expected {shape}")
+    f32 = torch.float32
+    for name, t, n in (("input", x, M * K), ("scales", scales, N * K // group_size),
+                       ("output", y, M * out_cols)) + tuple(
+                           (nm, t, math.prod(sh)) for nm, t, sh in extra):
+        if t.dtype != f32:
+            raise ValueError(f"{name} dtype {t.dtype}, expected {f32}")
+        if t.numel() != n:
+            raise ValueError(f"{name} holds {t.numel()} values, expected {n}")
         if not t.is_contiguous():
             raise ValueError("sq8 tensors must be contiguous")
-    devs = {str(t.device) for t in (x, w, scales, y) + tuple(t for _, t, _ in extra)}
-    if len(devs) != 1:
-        raise ValueError(f"operands on different devices: {sorted(devs)}")
+        if t.device != x.device:
+            raise ValueError(f"{name} on {t.device}, input on {x.device}")
+    if w.device != x.device:
+        raise ValueError(f"weight on {w.device}, input on {x.device}")
     if x.device.type != "cuda":
         raise ValueError(f"operands on {x.device}, expected a GPU")
-
 
 def matmul(x, w, scales, y=None, group_size: int = 64, workspace: Workspace | None = None,
            stream=None):
