@@ -285,7 +285,7 @@ def copy_ceiling(torch, dev, shapes):
 
 
 def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed: int = 0,
-              sigma: float = 0.8, packed: bool = False):
+              sigma: float = 0.8, packed: bool = False, native: bool = True):
     """Config 5: continuous batching of n_seqs requests on the Llama-3-8B-shaped INT8 model (the
     step's random-init projections, plus a random embedding and unit norms). Prompt lengths are
     lognormal with median 200 (sigma 0.8, clipped to 16..2048), uniform random token ids,
@@ -312,26 +312,33 @@ def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed:
     prompts = [rng.integers(0, cfg.vocab, int(n)).tolist() for n in lens]
     max_seq = int(lens.max()) + n_new
     block = sch.Scheduler.resolve_block_size(float(lens.mean()))
+    num_blocks = 64 * ((max_seq + block - 1) // block)  # 64 full-length sequences
     s = sch.Scheduler(None, max_batch=64, max_seq_len=max_seq, max_gen_len=n_new,
-                      block_size=block)
+                      block_size=block, num_blocks=num_blocks)
     model = bm.PagedBatchModel(cfg, w, GS, max_rows=64, max_seq_len=max_seq,
-                               num_blocks=s.alloc.num_blocks, block_size=block, device=dev,
+                               num_blocks=num_blocks, block_size=block, device=dev,
                                packed=packed)
     # Decode-step graphs for every row count, captured at start-up (not timed).
     capture_s = model.capture_decode_graphs()
-    s.forward = model.forward
+    if native:  # the C++ scheduler (scheduler::Scheduler), the model called back per step
+        nat = importlib.import_module("llm_steadyinfer_amd.native_scheduler")
+        s = nat.NativeScheduler(model, max_batch=64, max_seq_len=max_seq, max_gen_len=n_new,
+                                block_size=block, num_blocks=num_blocks)
+    else:
+        s.forward = model.forward
     for p in ([5, 6, 7], [8, 9]):          # warm-up requests (every kernel once), not timed
         s.add_request(p)
     s.run()
-    s.finished.clear()
-    steps0, rows0 = s.steps, s.rows_run
+    warm = {q.id for q in s.finished}
+    steps0, rows0, pre0 = s.steps, s.rows_run, s.preemptions
     for p in prompts:
         s.add_request(p)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    done = s.run()
+    s.run()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    done = [q for q in s.finished if q.id not in warm]
     gen_tokens = sum(len(q.generated_tokens) for q in done)
     prompt_tokens = int(lens.sum())
     return {"workload": f"config 5: Llama-3-8B-shaped random-init INT8 model, {n_seqs} sequences, "
@@ -343,9 +350,10 @@ def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed:
             "total_tokens_per_s": round((gen_tokens + prompt_tokens) / wall, 1),
             "wall_s": round(wall, 3), "generated_tokens": gen_tokens,
             "prompt_tokens": prompt_tokens, "steps": s.steps - steps0,
-            "rows": s.rows_run - rows0, "preemptions": s.preemptions,
-            "kv_pool_GB": round(2 * 4 * cfg.layer_num * cfg.kv_dim * block * s.alloc.num_blocks
-                                / 1e9, 2),
+            "rows": s.rows_run - rows0, "preemptions": s.preemptions - pre0,
+            "scheduler": "native (C++ scheduler::Scheduler)" if native else "python",
+            "kv_pool_GB": round(2 * 4 * cfg.layer_num * cfg.kv_dim * block * num_blocks / 1e9,
+                                2),
             "graph_replays": model.graph_replays, "graph_capture_s": round(capture_s, 2),
             "launch": "decode-only steps: one HIP graph per row count (captured at start-up); "
                       "steps with prefill rows: eager; one host sync per step"}
@@ -362,6 +370,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-batch", action="store_true", help="skip config 5 (continuous batching)")
+    ap.add_argument("--py-scheduler", action="store_true",
+                    help="config 5 on the Python scheduler (default: the C++ scheduler)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--graph", action="store_true", help="replay the step as one HIP graph")
     ap.add_argument("--profile", action="store_true",
@@ -613,12 +623,13 @@ def main():
 
     batch = None
     if not args.no_batch:
-        batch = batch_run(torch, weights, lm_head)
+        batch = batch_run(torch, weights, lm_head, native=not args.py_scheduler)
         print(f"# batch done: {batch['output_tokens_per_s']} output tokens/s", file=sys.stderr,
               flush=True)
     batch_packed = None
     if args.packed and not args.no_batch:
-        batch_packed = batch_run(torch, weights, lm_head, packed=True)
+        batch_packed = batch_run(torch, weights, lm_head, packed=True,
+                                 native=not args.py_scheduler)
         print(f"# packed batch done: {batch_packed['output_tokens_per_s']} output tokens/s",
               file=sys.stderr, flush=True)
 

@@ -165,16 +165,29 @@ class PagedBatchModel:
     def forward(self, rows, tables: List[List[int]]) -> List[int]:
         """Run the batch rows (scheduler.BatchRow, decode rows first) and return the greedy token
         of each decode row."""
-        torch = self.torch
         B = len(rows)
-        if B == 0 or B > self.max_rows:
-            raise ValueError(f"{B} rows for a model sized for {self.max_rows}")
         nd = sum(1 for r in rows if r.is_decode)
+        if any(r.is_decode for r in rows[nd:]):
+            raise ValueError("decode rows must come first")
         tok = np.fromiter((r.token for r in rows), np.int32, B)
         pos = np.fromiter((r.position for r in rows), np.int32, B)
-        tab = np.asarray(tables, np.int32).reshape(B, -1)
+        return self.forward_arrays(tok, pos, np.asarray(tables, np.int32).reshape(B, -1), nd)
+
+    def forward_arrays(self, tok, pos, tab, nd: int) -> List[int]:
+        """The same step from int32 arrays: tokens and positions [B], block tables
+        [B][max_blocks_per_seq]; the first nd rows are the decode rows (the native scheduler's
+        callback hands its rows over this way)."""
+        torch = self.torch
+        B = len(tok)
+        if B == 0 or B > self.max_rows:
+            raise ValueError(f"{B} rows for a model sized for {self.max_rows}")
+        if len(pos) != B or tab.shape[0] != B or not 0 <= nd <= B:
+            raise ValueError("rows, positions, tables and decode count disagree")
         if tab.shape[1] != self.max_blocks_per_seq:
             raise ValueError("block-table width does not match max_seq_len / block_size")
+        tok = np.ascontiguousarray(tok, np.int32)
+        pos = np.ascontiguousarray(pos, np.int32)
+        tab = np.ascontiguousarray(tab, np.int32)
         self.tok[:B].copy_(torch.from_numpy(tok))
         self.pos[:B].copy_(torch.from_numpy(pos))
         self.table[:B].copy_(torch.from_numpy(tab))

@@ -1,0 +1,227 @@
+"""ctypes binding of the native continuous-batching scheduler (scheduler::Scheduler in
+libsq8_op.so, src/source/scheduler/scheduler.cpp's interface; C entry points in
+cpp/include/scheduler/scheduler_c.h).
+
+NativeScheduler takes the same arguments and exposes the same results as scheduler.Scheduler, and
+makes the same decisions step for step; the batching bookkeeping runs in C++ and calls the model
+back once per step. A model with ``forward_arrays(tokens, positions, tables, num_decode)`` (numpy
+int32 arrays; PagedBatchModel has it) gets the step's rows as arrays; otherwise it is called as
+``forward(rows, tables)`` with row objects like scheduler.BatchRow.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field
+from typing import Iterable, List, Optional
+
+import numpy as np
+
+from . import PKG_DIR
+
+OP_LIB_PATH = PKG_DIR / "libsq8_op.so"
+SCHED_SYMBOLS = ("sq8_sched_create", "sq8_sched_destroy", "sq8_sched_set_stop_tokens",
+                 "sq8_sched_add_request", "sq8_sched_step", "sq8_sched_run",
+                 "sq8_sched_all_finished", "sq8_sched_stats", "sq8_sched_generated",
+                 "sq8_sched_finished_ids", "sq8_sched_last_rows", "sq8_sched_block_ref",
+                 "sq8_sched_invariant")
+SQ8_SCHED_OK, SQ8_SCHED_ERR_ARG, SQ8_SCHED_ERR_MODEL, SQ8_SCHED_ERR_STEPS = 0, -1, -2, -3
+
+_P32 = ctypes.POINTER(ctypes.c_int32)
+FORWARD_FN = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _P32,
+                              _P32, _P32, _P32, ctypes.c_int, _P32)
+_lib = None
+
+
+def op_lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not OP_LIB_PATH.exists():
+            raise RuntimeError(f"C++ op library not built: {OP_LIB_PATH} "
+                               "(run __graft_entry__.build())")
+        L = ctypes.CDLL(str(OP_LIB_PATH))
+        vp, I = ctypes.c_void_p, ctypes.c_int
+        L.sq8_sched_create.argtypes = [I, I, I, I, I, I, FORWARD_FN, vp]
+        L.sq8_sched_create.restype = vp
+        L.sq8_sched_destroy.argtypes = [vp]
+        L.sq8_sched_destroy.restype = None
+        L.sq8_sched_set_stop_tokens.argtypes = [vp, _P32, I]
+        L.sq8_sched_add_request.argtypes = [vp, _P32, I]
+        L.sq8_sched_step.argtypes = [vp]
+        L.sq8_sched_run.argtypes = [vp, I]
+        L.sq8_sched_all_finished.argtypes = [vp]
+        L.sq8_sched_stats.argtypes = [vp, ctypes.POINTER(ctypes.c_int64), I]
+        L.sq8_sched_generated.argtypes = [vp, I, _P32, I]
+        L.sq8_sched_finished_ids.argtypes = [vp, _P32, I]
+        L.sq8_sched_last_rows.argtypes = [vp, _P32, I]
+        L.sq8_sched_block_ref.argtypes = [vp, I]
+        L.sq8_sched_invariant.argtypes = [vp]
+        for name in SCHED_SYMBOLS:
+            if name not in ("sq8_sched_create", "sq8_sched_destroy"):
+                getattr(L, name).restype = I
+        _lib = L
+    return _lib
+
+
+def _i32(a) -> "ctypes.Array":
+    a = np.ascontiguousarray(a, dtype=np.int32)
+    return a, a.ctypes.data_as(_P32)
+
+
+@dataclass
+class SeqRef:
+    id: int
+
+
+@dataclass
+class Row:
+    """One batch row handed to a row-based forward (the fields of scheduler.BatchRow)."""
+    seq: SeqRef
+    is_decode: bool
+    token: int
+    position: int
+
+
+@dataclass
+class FinishedSequence:
+    id: int
+    prompt_tokens: List[int]
+    generated_tokens: List[int] = field(default_factory=list)
+
+
+class NativeScheduler:
+    def __init__(self, forward, max_batch: int, max_seq_len: int, max_gen_len: int = 0,
+                 block_size: int = 16, num_blocks: Optional[int] = None,
+                 prefix_cache: bool = False, stop_tokens: Iterable[int] = ()):
+        L = op_lib()
+        self.forward = forward
+        self.max_batch, self.max_seq_len, self.block_size = max_batch, max_seq_len, block_size
+        self.max_blocks_per_seq = (max_seq_len + block_size - 1) // block_size
+        self._error = None
+        self._cb = FORWARD_FN(self._forward)  # kept alive as long as the handle
+        self._h = L.sq8_sched_create(max_batch, max_seq_len, max_gen_len, block_size,
+                                     num_blocks or 0, int(bool(prefix_cache)), self._cb, None)
+        if not self._h:
+            raise ValueError("bad scheduler arguments")
+        stop, p = _i32(list(stop_tokens))
+        self._check(L.sq8_sched_set_stop_tokens(self._h, p, len(stop)))
+        self._prompts = {}
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            op_lib().sq8_sched_destroy(h)
+            self._h = None
+
+    @staticmethod
+    def _check(rc):
+        if rc < 0:
+            raise RuntimeError(f"native scheduler status {rc}")
+        return rc
+
+    # ------------------------------------------------------------------ the model callback
+    def _forward(self, _user, batch, nd, tok_p, pos_p, ids_p, tab_p, stride, next_p):
+        try:
+            tok = np.ctypeslib.as_array(tok_p, (batch,)).copy()
+            pos = np.ctypeslib.as_array(pos_p, (batch,)).copy()
+            tab = np.ctypeslib.as_array(tab_p, (batch, stride)).copy()
+            if hasattr(self.forward, "forward_arrays"):
+                out = self.forward.forward_arrays(tok, pos, tab, nd)
+            else:
+                ids = np.ctypeslib.as_array(ids_p, (batch,))
+                rows = [Row(SeqRef(int(ids[i])), i < nd, int(tok[i]), int(pos[i]))
+                        for i in range(batch)]
+                out = self.forward(rows, tab.tolist())
+            if len(out) != nd:
+                raise RuntimeError(f"forward returned {len(out)} tokens for {nd} decode rows")
+            if nd:
+                np.ctypeslib.as_array(next_p, (nd,))[:] = np.asarray(out, dtype=np.int32)
+            return 0
+        except BaseException as e:  # noqa: BLE001 - reported by step()
+            self._error = e
+            return 1
+
+    # ------------------------------------------------------------------ Scheduler interface
+    def add_request(self, prompt: List[int]) -> int:
+        arr, p = _i32(list(prompt))
+        sid = op_lib().sq8_sched_add_request(self._h, p, len(arr))
+        if sid >= 0:
+            self._prompts[sid] = [int(t) for t in prompt]
+        return sid
+
+    def step(self) -> None:
+        rc = op_lib().sq8_sched_step(self._h)
+        if rc == SQ8_SCHED_ERR_MODEL and self._error is not None:
+            e, self._error = self._error, None
+            raise e
+        self._check(rc)
+
+    def all_finished(self) -> bool:
+        return bool(self._check(op_lib().sq8_sched_all_finished(self._h)))
+
+    def run(self, max_steps: Optional[int] = None) -> List[FinishedSequence]:
+        """Step until every request finished (RuntimeError after max_steps steps)."""
+        while not self.all_finished():
+            if max_steps is not None and self.steps >= max_steps:
+                raise RuntimeError(f"scheduler made no progress within {max_steps} steps")
+            self.step()
+        return sorted(self.finished, key=lambda s: s.id)
+
+    def _stats(self):
+        out = (ctypes.c_int64 * 10)()
+        self._check(op_lib().sq8_sched_stats(self._h, out, 10))
+        return list(out)
+
+    @property
+    def steps(self) -> int:
+        return self._stats()[0]
+
+    @property
+    def rows_run(self) -> int:
+        return self._stats()[1]
+
+    @property
+    def preemptions(self) -> int:
+        return self._stats()[2]
+
+    @property
+    def shared_prefix_blocks(self) -> int:
+        return self._stats()[3]
+
+    @property
+    def prefill_budget(self) -> int:
+        return self._stats()[7]
+
+    def free_block_count(self) -> int:
+        return self._stats()[8]
+
+    def prefix_entries(self) -> int:
+        return self._stats()[9]
+
+    def generated(self, seq_id: int) -> List[int]:
+        L = op_lib()
+        n = self._check(L.sq8_sched_generated(self._h, seq_id, None, 0))
+        buf = (ctypes.c_int32 * max(n, 1))()
+        L.sq8_sched_generated(self._h, seq_id, buf, n)
+        return list(buf[:n])
+
+    @property
+    def finished(self) -> List[FinishedSequence]:
+        L = op_lib()
+        n = self._check(L.sq8_sched_finished_ids(self._h, None, 0))
+        buf = (ctypes.c_int32 * max(n, 1))()
+        L.sq8_sched_finished_ids(self._h, buf, n)
+        return [FinishedSequence(i, self._prompts[i], self.generated(i)) for i in buf[:n]]
+
+    def last_rows(self):
+        """(seq id, is_decode, token, position) of each row of the last step."""
+        L = op_lib()
+        n = self._check(L.sq8_sched_last_rows(self._h, None, 0))
+        buf = (ctypes.c_int32 * max(4 * n, 1))()
+        L.sq8_sched_last_rows(self._h, buf, n)
+        return [tuple(buf[4 * i:4 * i + 4]) for i in range(n)]
+
+    def block_ref(self, block: int) -> int:
+        return self._check(op_lib().sq8_sched_block_ref(self._h, block))
+
+    def invariant_holds(self) -> bool:
+        return bool(self._check(op_lib().sq8_sched_invariant(self._h)))
