@@ -163,3 +163,28 @@ def test_native_run_bounds_steps():
     s.add_request([1, 2])
     with pytest.raises(RuntimeError, match="no progress"):
         s.run(max_steps=3)
+
+
+def test_cpp_scheduler_program_under_sanitizers(tmp_path):
+    """tests/cpp/test_scheduler.cpp: 300 randomised workloads through scheduler::Scheduler with a
+    C++ chain model, every sequence's tokens against its single-sequence run, built with g++
+    -fsanitize=address,undefined (host code only)."""
+    import shutil
+    import subprocess
+    from conftest import REPO
+    if shutil.which("g++") is None:
+        pytest.skip("g++ not available")
+    cpp = REPO / "llm-steadyinfer_amd" / "cpp"
+    exe = tmp_path / "test_scheduler"
+    cmd = ["g++", "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined",
+           "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer",
+           "-I", str(cpp / "include"), "-I", str(REPO / "tests" / "cpp"),
+           str(REPO / "tests" / "cpp" / "test_scheduler.cpp")] + \
+          [str(cpp / "src" / f) for f in ("scheduler.cpp", "block_allocator.cpp",
+                                          "prefix_cache.cpp")] + ["-o", str(exe)]
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stderr[-3000:]
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    print(res.stdout[-2000:])
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-3000:]
+    assert "scheduler: 0 failure(s)" in res.stdout
