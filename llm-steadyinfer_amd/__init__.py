@@ -492,12 +492,43 @@ def decode_attention_workspace_bytes(head_num: int, head_size: int, max_seq: int
 # Thin wrappers over include/sq8_batch.h (continuous batching, paged KV cache).
 
 
+def _check_paged(qkv, q_width: int, head_num: int, kv_head_num: int, head_size: int, positions,
+                 block_table, block_size: int, kcache, vcache, out=None):
+    """Shape checks of the paged operators before launch (the kernels index every buffer from
+    these sizes; the reference checks them in its batched forward, llama3.cpp:996-1062)."""
+    import torch
+    rows = positions.numel()
+    dim, kv_dim = head_num * head_size, kv_head_num * head_size
+    if head_num <= 0 or kv_head_num <= 0 or head_num % kv_head_num != 0:
+        raise ValueError(f"{head_num} query heads over {kv_head_num} kv heads")
+    if positions.dtype != torch.int32 or block_table.dtype != torch.int32:
+        raise ValueError("positions and block tables must be int32")
+    if block_table.dim() != 2 or block_table.shape[0] < rows:
+        raise ValueError(f"block table {tuple(block_table.shape)} for {rows} rows")
+    if q_width < dim + 2 * kv_dim or qkv.numel() < (rows - 1) * q_width + dim + 2 * kv_dim:
+        raise ValueError(f"qkv of {qkv.numel()} values for {rows} rows of width {q_width}")
+    for name, c in (("key cache", kcache), ("value cache", vcache)):
+        if c.dim() != 3 or c.shape[1] != block_size or c.shape[2] != kv_dim:
+            raise ValueError(f"{name} {tuple(c.shape)}, expected [blocks][{block_size}][{kv_dim}]")
+    if out is not None and out.numel() < rows * dim:
+        raise ValueError(f"output of {out.numel()} values for {rows} rows of {dim}")
+    for t in (qkv, positions, block_table, kcache, vcache) + (() if out is None else (out,)):
+        if not t.is_contiguous():
+            raise ValueError("sq8 tensors must be contiguous")
+        if t.dtype not in (torch.float32, torch.int32):
+            raise ValueError(f"unexpected dtype {t.dtype}")
+
+
 def paged_rope_kv(qkv, head_num: int, kv_head_num: int, head_size: int, positions, block_table,
                   block_size: int, sin_cache, cos_cache, kcache, vcache, stream=None):
     """Rows of qkv ([rows][dim + 2 kv_dim]) at their positions: rotate q in place, write the
     rotated k and v to the rows' paged cache slots. positions int32 [rows], block_table int32
     [rows][stride]; kcache/vcache [num_blocks][block_size][kv_dim] of one layer."""
     rows = positions.numel()
+    if qkv.shape[-1] != (head_num + 2 * kv_head_num) * head_size:
+        raise ValueError(f"qkv rows of {qkv.shape[-1]} values, expected q, k and v exactly")
+    _check_paged(qkv, qkv.shape[-1], head_num, kv_head_num, head_size, positions, block_table,
+                 block_size, kcache, vcache)
     _call("sq8_paged_rope_kv", _ptr(qkv), rows, head_num, kv_head_num, head_size, _ptr(positions),
           _ptr(block_table), block_table.shape[-1], block_size, _ptr(sin_cache), _ptr(cos_cache),
           _ptr(kcache), _ptr(vcache), stream=stream)
@@ -517,6 +548,8 @@ def paged_attention(qkv, q_stride: int, head_num: int, kv_head_num: int, head_si
     With a workspace (zero-filled before its first use, of at least
     paged_attention_workspace_bytes() bytes) long rows split over several workgroups."""
     rows = positions.numel()
+    _check_paged(qkv, q_stride, head_num, kv_head_num, head_size, positions, block_table,
+                 block_size, kcache, vcache, out)
     if workspace is None:
         _call("sq8_paged_attention", _ptr(qkv), q_stride, rows, head_num, kv_head_num, head_size,
               _ptr(positions), _ptr(block_table), block_table.shape[-1], block_size,

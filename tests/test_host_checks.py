@@ -70,3 +70,38 @@ def test_packed_weight_shape_is_checked():
     pw = sq8.PackedWeight(torch.zeros(N * K, dtype=torch.int8), N, K + 64)
     with pytest.raises(ValueError, match="weight shape"):
         sq8.matmul(t["x"], pw, t["s"], t["y"], group_size=GS)
+
+
+def _paged(rows=3, heads=4, kv_heads=2, hs=64, bs=16, width=8, nb=10, **over):
+    t = dict(qkv=torch.zeros(rows, (heads + 2 * kv_heads) * hs),
+             pos=torch.zeros(rows, dtype=torch.int32),
+             tab=torch.zeros(rows, width, dtype=torch.int32),
+             kc=torch.zeros(nb, bs, kv_heads * hs), vc=torch.zeros(nb, bs, kv_heads * hs),
+             out=torch.zeros(rows, heads * hs))
+    t.update(over)
+    return t
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(pos=torch.zeros(3, dtype=torch.int64)), "int32"),
+    (dict(tab=torch.zeros(2, 8, dtype=torch.int32)), "block table"),
+    (dict(kc=torch.zeros(10, 8, 128)), "key cache"),
+    (dict(vc=torch.zeros(10, 16, 64)), "value cache"),
+    (dict(out=torch.zeros(3, 100)), "output of"),
+    (dict(qkv=torch.zeros(2, 512)), "qkv of"),
+])
+def test_paged_attention_checks_shapes(over, msg):
+    t = _paged(**over)
+    with pytest.raises(ValueError, match=msg):
+        sq8.paged_attention(t["qkv"], 512, 4, 2, 64, t["pos"], t["tab"], 16, t["kc"], t["vc"],
+                            t["out"])
+
+
+def test_paged_rope_kv_checks_shapes():
+    t = _paged(qkv=torch.zeros(3, 515))
+    with pytest.raises(ValueError, match="q, k and v exactly"):
+        sq8.paged_rope_kv(t["qkv"], 4, 2, 64, t["pos"], t["tab"], 16, None, None, t["kc"],
+                          t["vc"])
+    with pytest.raises(ValueError, match="query heads"):
+        sq8.paged_rope_kv(torch.zeros(3, 64 * 9), 5, 2, 64, t["pos"], t["tab"], 16, None, None,
+                          t["kc"], t["vc"])
