@@ -24,12 +24,6 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off /= 2) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
-}
-
 // Sum over a workgroup of W waves; every thread gets the total. `red` holds W floats.
 template <int W = kBlockWaves>
 __device__ __forceinline__ float block_sum(float v, float* red) {
@@ -41,19 +35,6 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
   float t = red[0];
 #pragma unroll
   for (int i = 1; i < W; ++i) t += red[i];
-  return t;
-}
-
-template <int W = kBlockWaves>
-__device__ __forceinline__ float block_max(float v, float* red) {
-  v = wave_max(v);
-  const int wave = threadIdx.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & (kWave - 1)) == 0) red[wave] = v;
-  __syncthreads();
-  float t = red[0];
-#pragma unroll
-  for (int i = 1; i < W; ++i) t = fmaxf(t, red[i]);
   return t;
 }
 
