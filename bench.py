@@ -285,7 +285,8 @@ def copy_ceiling(torch, dev, shapes):
 
 
 def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed: int = 0,
-              sigma: float = 0.8, packed: bool = False, native: bool = True):
+              sigma: float = 0.8, packed: bool = False, native: bool = True,
+              native_model: bool = False):
     """Config 5: continuous batching of n_seqs requests on the Llama-3-8B-shaped INT8 model (the
     step's random-init projections, plus a random embedding and unit norms). Prompt lengths are
     lognormal with median 200 (sigma 0.8, clipped to 16..2048), uniform random token ids,
@@ -315,9 +316,16 @@ def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed:
     num_blocks = 64 * ((max_seq + block - 1) // block)  # 64 full-length sequences
     s = sch.Scheduler(None, max_batch=64, max_seq_len=max_seq, max_gen_len=n_new,
                       block_size=block, num_blocks=num_blocks)
-    model = bm.PagedBatchModel(cfg, w, GS, max_rows=64, max_seq_len=max_seq,
-                               num_blocks=num_blocks, block_size=block, device=dev,
-                               packed=packed)
+    if native_model:  # model::PagedBatchModel (C++): the scheduler calls it with no Python
+        nat = importlib.import_module("llm_steadyinfer_amd.native_scheduler")
+        model = nat.NativePagedBatchModel(cfg, w, GS, max_rows=64, max_seq_len=max_seq,
+                                          num_blocks=num_blocks, block_size=block, device=dev,
+                                          packed=packed)
+        native = True
+    else:
+        model = bm.PagedBatchModel(cfg, w, GS, max_rows=64, max_seq_len=max_seq,
+                                   num_blocks=num_blocks, block_size=block, device=dev,
+                                   packed=packed)
     # Decode-step graphs for every row count, captured at start-up (not timed).
     capture_s = model.capture_decode_graphs()
     if native:  # the C++ scheduler (scheduler::Scheduler), the model called back per step
@@ -352,6 +360,7 @@ def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed:
             "prompt_tokens": prompt_tokens, "steps": s.steps - steps0,
             "rows": s.rows_run - rows0, "preemptions": s.preemptions - pre0,
             "scheduler": "native (C++ scheduler::Scheduler)" if native else "python",
+            "model": "native (C++ model::PagedBatchModel)" if native_model else "python",
             "kv_pool_GB": round(2 * 4 * cfg.layer_num * cfg.kv_dim * block * num_blocks / 1e9,
                                 2),
             "graph_replays": model.graph_replays, "graph_capture_s": round(capture_s, 2),
@@ -372,6 +381,8 @@ def main():
     ap.add_argument("--no-batch", action="store_true", help="skip config 5 (continuous batching)")
     ap.add_argument("--py-scheduler", action="store_true",
                     help="config 5 on the Python scheduler (default: the C++ scheduler)")
+    ap.add_argument("--native-model", action="store_true",
+                    help="config 5 on the C++ batch model as well (no Python in the step loop)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--graph", action="store_true", help="replay the step as one HIP graph")
     ap.add_argument("--profile", action="store_true",
@@ -623,13 +634,15 @@ def main():
 
     batch = None
     if not args.no_batch:
-        batch = batch_run(torch, weights, lm_head, native=not args.py_scheduler)
+        batch = batch_run(torch, weights, lm_head, native=not args.py_scheduler,
+                          native_model=args.native_model)
         print(f"# batch done: {batch['output_tokens_per_s']} output tokens/s", file=sys.stderr,
               flush=True)
     batch_packed = None
     if args.packed and not args.no_batch:
         batch_packed = batch_run(torch, weights, lm_head, packed=True,
-                                 native=not args.py_scheduler)
+                                 native=not args.py_scheduler,
+                                 native_model=args.native_model)
         print(f"# packed batch done: {batch_packed['output_tokens_per_s']} output tokens/s",
               file=sys.stderr, flush=True)
 

@@ -97,9 +97,16 @@ class NativeScheduler:
         self.max_batch, self.max_seq_len, self.block_size = max_batch, max_seq_len, block_size
         self.max_blocks_per_seq = (max_seq_len + block_size - 1) // block_size
         self._error = None
-        self._cb = FORWARD_FN(self._forward)  # kept alive as long as the handle
+        native = getattr(forward, "native_forward", None)
+        if native is not None:  # a native model: C++ calls C++, no Python in the step loop
+            self._cb = FORWARD_FN(native[0])
+            user = native[1]
+        else:
+            self._cb = FORWARD_FN(self._forward)  # kept alive as long as the handle
+            user = None
+        self._native = native is not None
         self._h = L.sq8_sched_create(max_batch, max_seq_len, max_gen_len, block_size,
-                                     num_blocks or 0, int(bool(prefix_cache)), self._cb, None)
+                                     num_blocks or 0, int(bool(prefix_cache)), self._cb, user)
         if not self._h:
             raise ValueError("bad scheduler arguments")
         stop, p = _i32(list(stop_tokens))
@@ -148,18 +155,34 @@ class NativeScheduler:
             self._prompts[sid] = [int(t) for t in prompt]
         return sid
 
-    def step(self) -> None:
-        rc = op_lib().sq8_sched_step(self._h)
-        if rc == SQ8_SCHED_ERR_MODEL and self._error is not None:
+    def _raise_model_error(self):
+        if self._error is not None:
             e, self._error = self._error, None
             raise e
+        if self._native:
+            raise RuntimeError("native model: " + self.forward.last_error())
+        raise RuntimeError("model forward failed")
+
+    def step(self) -> None:
+        rc = op_lib().sq8_sched_step(self._h)
+        if rc == SQ8_SCHED_ERR_MODEL:
+            self._raise_model_error()
         self._check(rc)
 
     def all_finished(self) -> bool:
         return bool(self._check(op_lib().sq8_sched_all_finished(self._h)))
 
     def run(self, max_steps: Optional[int] = None) -> List[FinishedSequence]:
-        """Step until every request finished (RuntimeError after max_steps steps)."""
+        """Step until every request finished (RuntimeError after max_steps steps). With a native
+        model the whole loop runs in C++ (sq8_sched_run)."""
+        if self._native:
+            rc = op_lib().sq8_sched_run(self._h, max_steps or 0)
+            if rc == SQ8_SCHED_ERR_STEPS:
+                raise RuntimeError(f"scheduler made no progress within {max_steps} steps")
+            if rc == SQ8_SCHED_ERR_MODEL:
+                self._raise_model_error()
+            self._check(rc)
+            return sorted(self.finished, key=lambda q: q.id)
         while not self.all_finished():
             if max_steps is not None and self.steps >= max_steps:
                 raise RuntimeError(f"scheduler made no progress within {max_steps} steps")
@@ -225,3 +248,133 @@ class NativeScheduler:
 
     def invariant_holds(self) -> bool:
         return bool(self._check(op_lib().sq8_sched_invariant(self._h)))
+
+
+class NativePagedBatchModel:
+    """model::PagedBatchModel (C++, libsq8_op.so) over the weights dict of
+    batch_model.PagedBatchModel (device tensors: "qkv", "o", "gu", "down" lists of (q, s) per
+    layer, "cls" (q, s), "emb", "norm" list of 2 L + 1). The same launches in the same order as
+    the Python model, from C++, on the model's own stream. With packed the projections are
+    repacked once (sq8_pack_weights) and the model holds the packed copies.
+
+    Handed to NativeScheduler, the scheduler calls it directly (native_forward); with the Python
+    scheduler, forward / forward_arrays go through ctypes."""
+
+    def __init__(self, cfg, weights: dict, group_size: int, max_rows: int, max_seq_len: int,
+                 num_blocks: int, block_size: int, device="cuda", use_graphs: bool = True,
+                 split_kv: bool = True, packed: bool = False, eps: float = 1e-6):
+        import torch
+        from . import pack_weights
+        L = op_lib()
+        _bind_model(L)
+        self.torch = torch
+        if packed:
+            weights = dict(weights)
+            for key in ("qkv", "o", "gu", "down"):
+                weights[key] = [(pack_weights(q), s) for q, s in weights[key]]
+            weights["cls"] = (pack_weights(weights["cls"][0]), weights["cls"][1])
+        self.w = weights  # the model reads these device buffers for its lifetime
+        self.max_rows, self.block_size = max_rows, block_size
+        self.max_blocks_per_seq = (max_seq_len + block_size - 1) // block_size
+        nl = cfg.layer_num
+        ptrs = lambda ts, T: (T * len(ts))(*[t.data_ptr() for t in ts])
+        P8, PF = ctypes.c_void_p, ctypes.c_void_p
+        c = ModelConfigC(cfg.dim, cfg.hidden_dim, nl, cfg.head_num, cfg.kv_head_num, cfg.vocab,
+                         float(cfg.rope_theta), group_size, eps)
+        arrs = {k: (ptrs([q for q, _ in weights[k]], P8), ptrs([s for _, s in weights[k]], PF))
+                for k in ("qkv", "o", "gu", "down")}
+        norm = ptrs(weights["norm"], PF)
+        err = ctypes.c_char_p()
+        self._h = L.sq8_batch_model_create(
+            ctypes.byref(c), arrs["qkv"][0], arrs["qkv"][1], arrs["o"][0], arrs["o"][1],
+            arrs["gu"][0], arrs["gu"][1], arrs["down"][0], arrs["down"][1],
+            weights["cls"][0].data_ptr(), weights["cls"][1].data_ptr(),
+            weights["emb"].data_ptr(), norm, int(packed), max_rows, max_seq_len, num_blocks,
+            block_size, int(use_graphs), int(split_kv), None, ctypes.byref(err))
+        if not self._h:
+            raise RuntimeError("native batch model: " + (err.value or b"?").decode())
+        self.native_forward = (ctypes.cast(L.sq8_batch_model_forward, ctypes.c_void_p).value,
+                               self._h)
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            op_lib().sq8_batch_model_destroy(h)
+            self._h = None
+
+    def last_error(self) -> str:
+        return op_lib().sq8_batch_model_last_error(self._h).decode()
+
+    def capture_decode_graphs(self) -> float:
+        import time
+        t0 = time.perf_counter()
+        if op_lib().sq8_batch_model_capture_decode_graphs(self._h):
+            raise RuntimeError("native batch model: " + self.last_error())
+        return time.perf_counter() - t0
+
+    def _stats(self):
+        out = (ctypes.c_int64 * 3)()
+        op_lib().sq8_batch_model_stats(self._h, out, 3)
+        return list(out)
+
+    @property
+    def graph_replays(self) -> int:
+        return self._stats()[0]
+
+    @property
+    def rows_run(self) -> int:
+        return self._stats()[1]
+
+    @property
+    def graphs(self):
+        return range(self._stats()[2])
+
+    def forward_arrays(self, tok, pos, tab, nd: int):
+        tok, tp = _i32(tok)
+        pos, pp = _i32(pos)
+        tab, bp = _i32(tab)
+        B = len(tok)
+        out = (ctypes.c_int32 * max(nd, 1))()
+        if op_lib().sq8_batch_model_forward(self._h, B, nd, tp, pp, None, bp, tab.shape[1], out):
+            raise RuntimeError("native batch model: " + self.last_error())
+        return list(out[:nd])
+
+    def forward(self, rows, tables):
+        nd = sum(1 for r in rows if r.is_decode)
+        return self.forward_arrays([r.token for r in rows], [r.position for r in rows],
+                                   np.asarray(tables, np.int32).reshape(len(rows), -1), nd)
+
+
+class ModelConfigC(ctypes.Structure):
+    _fields_ = [("dim", ctypes.c_int), ("hidden_dim", ctypes.c_int),
+                ("layer_num", ctypes.c_int), ("head_num", ctypes.c_int),
+                ("kv_head_num", ctypes.c_int), ("vocab_size", ctypes.c_int),
+                ("rope_theta", ctypes.c_float), ("group_size", ctypes.c_int),
+                ("eps", ctypes.c_float)]
+
+
+MODEL_SYMBOLS = ("sq8_batch_model_create", "sq8_batch_model_destroy", "sq8_batch_model_forward",
+                 "sq8_batch_model_capture_decode_graphs", "sq8_batch_model_stats",
+                 "sq8_batch_model_last_error")
+_model_bound = False
+
+
+def _bind_model(L):
+    global _model_bound
+    if _model_bound:
+        return
+    vp, I = ctypes.c_void_p, ctypes.c_int
+    L.sq8_batch_model_create.argtypes = [ctypes.POINTER(ModelConfigC)] + [vp] * 12 + \
+        [I, I, I, I, I, I, I, vp, ctypes.POINTER(ctypes.c_char_p)]
+    L.sq8_batch_model_create.restype = vp
+    L.sq8_batch_model_destroy.argtypes = [vp]
+    L.sq8_batch_model_destroy.restype = None
+    L.sq8_batch_model_forward.argtypes = [vp, I, I, _P32, _P32, _P32, _P32, I, _P32]
+    L.sq8_batch_model_forward.restype = I
+    L.sq8_batch_model_capture_decode_graphs.argtypes = [vp]
+    L.sq8_batch_model_capture_decode_graphs.restype = I
+    L.sq8_batch_model_stats.argtypes = [vp, ctypes.POINTER(ctypes.c_int64), I]
+    L.sq8_batch_model_stats.restype = I
+    L.sq8_batch_model_last_error.argtypes = [vp]
+    L.sq8_batch_model_last_error.restype = ctypes.c_char_p
+    _model_bound = True

@@ -1,0 +1,152 @@
+// Recording stand-in for libsq8's C ABI (include/sq8*.h) for CPU tests of host code that issues
+// its launches (model::PagedBatchModel): each call appends one line, the function name and its
+// arguments, to a log, with pointers numbered in order of first appearance (so two hosts that
+// use their buffers in the same roles print the same log) and without the stream argument.
+// Workspace queries return fixed sizes and the fused-epilogue queries a fixed rule (fused when
+// M > 4 and N is even), restated by tests/test_native_scheduler.py for the Python model.
+#include <cstdio>
+#include <map>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "../../include/sq8.h"
+#include "../../include/sq8_batch.h"
+#include "../../include/sq8_decode.h"
+#include "hip/hip_runtime.h"
+
+namespace {
+std::map<const void*, int> g_ids;
+std::vector<std::string> g_log;
+
+struct Line {
+  std::ostringstream os;
+  explicit Line(const char* name) { os << name; }
+  Line& p(const void* v) {
+    if (!v) {
+      os << " 0";
+    } else {
+      auto it = g_ids.find(v);
+      if (it == g_ids.end()) it = g_ids.emplace(v, static_cast<int>(g_ids.size()) + 1).first;
+      os << " p" << it->second;
+    }
+    return *this;
+  }
+  Line& i(long long v) {
+    os << " " << v;
+    return *this;
+  }
+  Line& f(float v) {
+    char b[32];
+    std::snprintf(b, sizeof b, " %.6g", v);
+    os << b;
+    return *this;
+  }
+  ~Line() { g_log.push_back(os.str()); }
+};
+}  // namespace
+
+hipError_t hipGraphLaunch(hipGraphExec_t, hipStream_t) {
+  Line("graph_launch");
+  return hipSuccess;
+}
+void mock_print_log() {
+  for (const std::string& s : g_log) std::printf("%s\n", s.c_str());
+}
+void mock_mark(const char* what) { Line l(what); }
+
+extern "C" {
+const char* sq8_status_string(int) { return "mock"; }
+int sq8_epilogue_fused(int M, int N, int, int) { return M > 4 && N % 2 == 0; }
+int sq8_epilogue_packed_fused(int M, int N, int, int) { return M > 4 && N % 2 == 0; }
+size_t sq8_epilogue_workspace_bytes(int, int, int, int, int) { return 4096; }
+size_t sq8_epilogue_packed_workspace_bytes(int, int, int, int, int) { return 8192; }
+size_t sq8_rmsnorm_rows_workspace_bytes(int, int, int, int, int) { return 4096; }
+size_t sq8_rmsnorm_rows_packed_workspace_bytes(int, int, int, int, int) { return 8192; }
+size_t sq8_paged_attention_workspace_bytes(int, int, int, int, int, int) { return 2048; }
+
+int sq8_matmul(const float* x, const int8_t* w, const float* s, float* y, int M, int N, int K,
+               int gs, void* ws, size_t wsb, void*) {
+  Line("sq8_matmul").p(x).p(w).p(s).p(y).i(M).i(N).i(K).i(gs).p(ws).i(wsb);
+  return 0;
+}
+int sq8_matmul_packed(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
+                      int K, int gs, void* ws, size_t wsb, void*) {
+  Line("sq8_matmul_packed").p(x).p(w).p(s).p(y).i(M).i(N).i(K).i(gs).p(ws).i(wsb);
+  return 0;
+}
+int sq8_matmul_epilogue(const float* x, const int8_t* w, const float* s, float* y, int M, int N,
+                        int K, int gs, int epi, const float* r, void* ws, size_t wsb, void*) {
+  Line("sq8_matmul_epilogue").p(x).p(w).p(s).p(y).i(M).i(N).i(K).i(gs).i(epi).p(r).p(ws).i(wsb);
+  return 0;
+}
+int sq8_matmul_epilogue_packed(const float* x, const int8_t* w, const float* s, float* y, int M,
+                               int N, int K, int gs, int epi, const float* r, void* ws,
+                               size_t wsb, void*) {
+  Line("sq8_matmul_epilogue_packed").p(x).p(w).p(s).p(y).i(M).i(N).i(K).i(gs).i(epi).p(r).p(ws)
+      .i(wsb);
+  return 0;
+}
+int sq8_matmul_rmsnorm_rows(float* x, const float* res, const float* nw, float eps,
+                            const int8_t* w, const float* s, float* y, int M, int N, int K,
+                            int gs, int epi, void* ws, size_t wsb, void*) {
+  Line("sq8_matmul_rmsnorm_rows").p(x).p(res).p(nw).f(eps).p(w).p(s).p(y).i(M).i(N).i(K).i(gs)
+      .i(epi).p(ws).i(wsb);
+  return 0;
+}
+int sq8_matmul_rmsnorm_rows_packed(float* x, const float* res, const float* nw, float eps,
+                                   const int8_t* w, const float* s, float* y, int M, int N,
+                                   int K, int gs, int epi, void* ws, size_t wsb, void*) {
+  Line("sq8_matmul_rmsnorm_rows_packed").p(x).p(res).p(nw).f(eps).p(w).p(s).p(y).i(M).i(N).i(K)
+      .i(gs).i(epi).p(ws).i(wsb);
+  return 0;
+}
+int sq8_embedding(const float* t, int vocab, int dim, const int32_t* tok, int n, float* out,
+                  void*) {
+  Line("sq8_embedding").p(t).i(vocab).i(dim).p(tok).i(n).p(out);
+  return 0;
+}
+int sq8_rmsnorm(const float* x, const float* w, float* out, int rows, int dim, float eps, void*) {
+  Line("sq8_rmsnorm").p(x).p(w).p(out).i(rows).i(dim).f(eps);
+  return 0;
+}
+int sq8_add_rmsnorm(float* x, const float* r, const float* w, float* out, int rows, int dim,
+                    float eps, void*) {
+  Line("sq8_add_rmsnorm").p(x).p(r).p(w).p(out).i(rows).i(dim).f(eps);
+  return 0;
+}
+int sq8_rope_tables(float* s, float* c, int hs, int max_seq, float theta, void*) {
+  Line("sq8_rope_tables").p(s).p(c).i(hs).i(max_seq).f(theta);
+  return 0;
+}
+int sq8_paged_rope_kv(float* qkv, int rows, int h, int kvh, int hs, const int32_t* pos,
+                      const int32_t* tab, int stride, int bs, const float* sn, const float* cs,
+                      float* kc, float* vc, void*) {
+  Line("sq8_paged_rope_kv").p(qkv).i(rows).i(h).i(kvh).i(hs).p(pos).p(tab).i(stride).i(bs).p(sn)
+      .p(cs).p(kc).p(vc);
+  return 0;
+}
+int sq8_paged_attention(const float* qkv, int qs, int rows, int h, int kvh, int hs,
+                        const int32_t* pos, const int32_t* tab, int stride, int bs,
+                        const float* kc, const float* vc, float* out, void*) {
+  Line("sq8_paged_attention").p(qkv).i(qs).i(rows).i(h).i(kvh).i(hs).p(pos).p(tab).i(stride)
+      .i(bs).p(kc).p(vc).p(out);
+  return 0;
+}
+int sq8_paged_attention_ws(const float* qkv, int qs, int rows, int h, int kvh, int hs,
+                           const int32_t* pos, const int32_t* tab, int stride, int bs,
+                           const float* kc, const float* vc, float* out, void* ws, size_t wsb,
+                           void*) {
+  Line("sq8_paged_attention_ws").p(qkv).i(qs).i(rows).i(h).i(kvh).i(hs).p(pos).p(tab).i(stride)
+      .i(bs).p(kc).p(vc).p(out).p(ws).i(wsb);
+  return 0;
+}
+int sq8_swiglu_rows(const float* gu, int rows, int ffn, float* out, void*) {
+  Line("sq8_swiglu_rows").p(gu).i(rows).i(ffn).p(out);
+  return 0;
+}
+int sq8_argmax_rows(const float* logits, int rows, int n, int32_t* out, void*) {
+  Line("sq8_argmax_rows").p(logits).i(rows).i(n).p(out);
+  return 0;
+}
+}  // extern "C"

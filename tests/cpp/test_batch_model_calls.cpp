@@ -1,0 +1,82 @@
+// Prints the libsq8 calls model::PagedBatchModel issues for a scripted sequence of steps, built
+// with g++ against host stand-ins of the HIP runtime (tests/cpp/mock_hip) and of libsq8
+// (tests/cpp/mock_sq8.cpp). tests/test_native_scheduler.py compares the log with the calls the
+// Python PagedBatchModel issues for the same steps.
+//
+// stdin: "packed use_graphs split_kv", then per step "B nd", B tokens, B positions and
+// B * table_stride block-table entries; "capture" instead of a step calls
+// capture_decode_graphs(). Model: dim 64, FFN 96, 2 layers, 4 / 2 heads, vocab 50, 8 rows,
+// max_seq 64, 40 blocks of 4.
+#include <cstdio>
+#include <cstdlib>
+#include <iostream>
+#include <string>
+#include <vector>
+
+#include "model/paged_batch_model.h"
+
+void mock_print_log();
+void mock_mark(const char* what);
+
+int main() {
+  int packed = 0, graphs = 0, split = 0;
+  if (!(std::cin >> packed >> graphs >> split)) return 2;
+  model::BatchModelConfig c;
+  c.dim = 64;
+  c.hidden_dim = 96;
+  c.layer_num = 2;
+  c.head_num = 4;
+  c.kv_head_num = 2;
+  c.vocab_size = 50;
+  c.rope_theta = 1e6f;
+  c.group_size = 64;
+  std::vector<void*> bufs;
+  auto fake = [&]() {
+    bufs.push_back(std::malloc(64));
+    return bufs.back();
+  };
+  model::BatchModelWeights w;
+  // Allocation order mirrors the Python test's weight dict: per kind, per layer, (q, s).
+  for (auto* v : {&w.qkv, &w.o, &w.gu, &w.down})
+    for (int l = 0; l < c.layer_num; ++l)
+      v->push_back({static_cast<const int8_t*>(fake()), static_cast<const float*>(fake())});
+  w.cls = {static_cast<const int8_t*>(fake()), static_cast<const float*>(fake())};
+  w.embedding = static_cast<const float*>(fake());
+  for (int i = 0; i < 2 * c.layer_num + 1; ++i) w.norm.push_back(static_cast<const float*>(fake()));
+  w.packed = packed != 0;
+  model::PagedBatchModel m(c, w, 8, 64, 40, 4, nullptr, graphs != 0, split != 0);
+  base::Status st = m.init();
+  if (!st) {
+    std::printf("init failed: %s\n", st.get_err_msg().c_str());
+    return 1;
+  }
+  const int stride = m.max_blocks_per_seq();
+  std::string word;
+  while (std::cin >> word) {
+    if (word == "capture") {
+      mock_mark("capture_decode_graphs");
+      st = m.capture_decode_graphs();
+      if (!st) {
+        std::printf("capture failed: %s\n", st.get_err_msg().c_str());
+        return 1;
+      }
+      continue;
+    }
+    const int B = std::atoi(word.c_str());
+    int nd = 0;
+    std::cin >> nd;
+    std::vector<int32_t> tok(B), pos(B), tab(static_cast<size_t>(B) * stride), next(B);
+    for (auto& t : tok) std::cin >> t;
+    for (auto& p : pos) std::cin >> p;
+    for (auto& t : tab) std::cin >> t;
+    mock_mark("step");
+    st = m.forward_batch(B, nd, tok.data(), pos.data(), nullptr, tab.data(), stride, next.data());
+    if (!st) {
+      std::printf("step failed: %s\n", st.get_err_msg().c_str());
+      return 1;
+    }
+  }
+  mock_print_log();
+  for (void* p : bufs) std::free(p);
+  return 0;
+}

@@ -7,6 +7,7 @@ earlier token), checks that no row writes into a block another row also referenc
 a decode row's stored value as its token. Both schedulers must hand it the same rows and block
 tables at every step of randomised workloads (staggered arrivals, pools small enough to preempt,
 shared prefixes, stop tokens), end with the same tokens and counters, and return every block."""
+import ctypes
 import importlib
 
 import numpy as np
@@ -188,3 +189,210 @@ def test_cpp_scheduler_program_under_sanitizers(tmp_path):
     print(res.stdout[-2000:])
     assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-3000:]
     assert "scheduler: 0 failure(s)" in res.stdout
+
+
+def test_native_model_binding_rejects_bad_configuration():
+    """sq8_batch_model_create validates the configuration before touching the device."""
+    import torch
+    mf = importlib.import_module("llm_steadyinfer_amd.model_file")
+    cfg = mf.ModelConfig(dim=256, hidden_dim=512, layer_num=1, head_num=3, kv_head_num=2,
+                         vocab_size=-100, seq_len=64, rope_theta=1e4)  # 3 heads over 2 kv heads
+    t = torch.zeros(16)
+    w = {k: [(t, t)] for k in ("qkv", "o", "gu", "down")}
+    w.update(cls=(t, t), emb=t, norm=[t, t, t])
+    with pytest.raises(RuntimeError, match="model configuration"):
+        native.NativePagedBatchModel(cfg, w, 64, max_rows=4, max_seq_len=64, num_blocks=16,
+                                     block_size=4)
+
+
+def test_native_scheduler_calls_a_native_forward_directly():
+    """A model exposing native_forward (a C function with the callback's signature) is called
+    from C++ with no Python in the loop; its failure surfaces as RuntimeError. Here the C
+    function is sq8_batch_model_forward on a NULL model, which fails every call."""
+    L = native.op_lib()
+    native._bind_model(L)
+
+    class Stub:
+        native_forward = (ctypes.cast(L.sq8_batch_model_forward, ctypes.c_void_p).value, None)
+
+        def last_error(self):
+            return "stub failed"
+
+    s = NativeScheduler(Stub(), max_batch=2, max_seq_len=32, block_size=4)
+    assert s.add_request([1, 2, 3]) == 0
+    with pytest.raises(RuntimeError, match="stub failed"):
+        s.run(max_steps=10)
+    assert s.all_finished() and s.free_block_count() == 16
+
+
+# ----------------------------------------------------------------------------- native model calls
+# Argument kinds of the logged libsq8 calls, in C order: p pointer, i integer, f float, s stream
+# (not logged). Workspace sizes and the fused-epilogue rule restate tests/cpp/mock_sq8.cpp.
+_SPEC = {
+    "sq8_matmul": "ppppiiiipis", "sq8_matmul_packed": "ppppiiiipis",
+    "sq8_matmul_epilogue": "ppppiiiiippis", "sq8_matmul_epilogue_packed": "ppppiiiiippis",
+    "sq8_matmul_rmsnorm_rows": "pppfpppiiiiipis", "sq8_matmul_rmsnorm_rows_packed":
+    "pppfpppiiiiipis", "sq8_embedding": "piipips", "sq8_rmsnorm": "pppiifs",
+    "sq8_add_rmsnorm": "ppppiifs", "sq8_rope_tables": "ppiifs",
+    "sq8_paged_rope_kv": "piiiippiipppps", "sq8_paged_attention": "piiiiippiippps",
+    "sq8_paged_attention_ws": "piiiiippiippppis", "sq8_swiglu_rows": "piips",
+    "sq8_argmax_rows": "piips"}
+
+
+class _RecordingLib:
+    def __init__(self):
+        self.log, self.ids = [], {}
+
+    def _fmt(self, name, args):
+        out = [name]
+        for kind, a in zip(_SPEC[name], args):
+            if kind == "s":
+                continue
+            if kind == "p":
+                if not a:
+                    out.append("0")
+                else:
+                    out.append("p%d" % self.ids.setdefault(int(a), len(self.ids) + 1))
+            elif kind == "f":
+                out.append("%.6g" % np.float32(a))
+            else:
+                out.append(str(int(a)))
+        self.log.append(" ".join(out))
+        return 0
+
+    def __getattr__(self, name):
+        if name in _SPEC:
+            return lambda *a: self._fmt(name, a)
+        if name in ("sq8_epilogue_fused", "sq8_epilogue_packed_fused"):
+            return lambda M, N, K, gs: int(M > 4 and N % 2 == 0)
+        if name in ("sq8_epilogue_workspace_bytes", "sq8_rmsnorm_rows_workspace_bytes"):
+            return lambda *a: 4096
+        if name in ("sq8_epilogue_packed_workspace_bytes",
+                    "sq8_rmsnorm_rows_packed_workspace_bytes", "sq8_packed_workspace_bytes"):
+            return lambda *a: 8192
+        if name == "sq8_workspace_bytes":
+            return lambda *a: 4096
+        if name == "sq8_paged_attention_workspace_bytes":
+            return lambda *a: 2048
+        if name == "sq8_packed_weight_bytes":
+            return lambda N, K: ((N + 15) // 16) * 16 * K
+        if name == "sq8_pack_weights":
+            return lambda *a: 0
+        raise AttributeError(name)
+
+
+def _script(rng):
+    """Steps over a 40-block pool (blocks of 4, tables of 16): prefill-only, mixed,
+    decode-only at several row counts (twice at the same count), up to 8 rows."""
+    steps, pos_of = [], {}
+    tables = {s: [int(b) for b in rng.permutation(40)[:16]] for s in range(8)}
+    for B, nd in ((3, 0), (7, 2), (5, 5), (5, 5), (8, 3), (2, 2), (8, 8), (1, 0), (4, 4)):
+        seqs = rng.choice(8, B, replace=nd == B)
+        rows = []
+        for i, sq in enumerate(seqs):
+            p = pos_of.get(int(sq), 0)
+            pos_of[int(sq)] = p + 1
+            rows.append((int(rng.integers(0, 50)), min(p, 60), tables[int(sq)]))
+        steps.append((B, nd, rows))
+    return steps
+
+
+def _python_log(steps, packed, split):
+    import torch
+    pkg = load_pkg()
+    bm = importlib.import_module("llm_steadyinfer_amd.batch_model")
+    mf = importlib.import_module("llm_steadyinfer_amd.model_file")
+    rec = _RecordingLib()
+    saved = (pkg.lib, bm.lib, pkg._check_matmul, pkg._check_paged, torch.cuda.current_stream)
+
+    class _S:
+        cuda_stream = 0
+    try:
+        pkg.lib = bm.lib = lambda: rec
+        pkg._check_matmul = lambda *a, **k: None
+        pkg._check_paged = lambda *a, **k: None
+        torch.cuda.current_stream = lambda *a, **k: _S()
+        cfg = mf.ModelConfig(dim=64, hidden_dim=96, layer_num=2, head_num=4, kv_head_num=2,
+                             vocab_size=-50, seq_len=64, rope_theta=1e6)
+        q = lambda n, k: (torch.zeros((n, k), dtype=torch.int8), torch.zeros(n * k // 64))
+        w = {"qkv": [q(128, 64) for _ in range(2)], "o": [q(64, 64) for _ in range(2)],
+             "gu": [q(192, 64) for _ in range(2)], "down": [q(64, 96) for _ in range(2)],
+             "cls": q(50, 64), "emb": torch.zeros((50, 64)),
+             "norm": [torch.ones(64) for _ in range(5)]}
+        m = bm.PagedBatchModel(cfg, w, 64, max_rows=8, max_seq_len=64, num_blocks=40,
+                               block_size=4, device="cpu", use_graphs=False, split_kv=split,
+                               packed=packed)
+        for B, nd, rows in steps:
+            rec.log.append("step")
+            m.forward_arrays(np.array([r[0] for r in rows], np.int32),
+                             np.array([r[1] for r in rows], np.int32),
+                             np.array([r[2] for r in rows], np.int32), nd)
+    finally:
+        pkg.lib, bm.lib, pkg._check_matmul, pkg._check_paged, torch.cuda.current_stream = saved
+    return rec.log
+
+
+def _cpp_log(steps, packed, graphs, split, tmp_path, capture_first=False):
+    import shutil
+    import subprocess
+    from conftest import REPO
+    if shutil.which("g++") is None:
+        pytest.skip("g++ not available")
+    exe = tmp_path / "test_batch_model_calls"
+    if not exe.exists():
+        cpp = REPO / "llm-steadyinfer_amd" / "cpp"
+        t = REPO / "tests" / "cpp"
+        cmd = ["g++", "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined",
+               "-fno-sanitize-recover=undefined", "-I", str(t / "mock_hip"), "-I",
+               str(cpp / "include"), "-I", str(t), str(t / "test_batch_model_calls.cpp"),
+               str(t / "mock_sq8.cpp"), str(cpp / "src" / "paged_batch_model.cpp"), "-o", str(exe)]
+        res = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+        assert res.returncode == 0, res.stderr[-3000:]
+    lines = [f"{int(packed)} {int(graphs)} {int(split)}"] + (["capture"] if capture_first else [])
+    for B, nd, rows in steps:
+        lines.append(f"{B} {nd}")
+        lines.append(" ".join(str(r[0]) for r in rows))
+        lines.append(" ".join(str(r[1]) for r in rows))
+        lines.append(" ".join(str(b) for r in rows for b in r[2]))
+    res = subprocess.run([str(exe)], input="\n".join(lines) + "\n", capture_output=True,
+                         text=True, timeout=120)
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-3000:]
+    return res.stdout.splitlines()
+
+
+@pytest.mark.parametrize("packed,split", [(False, True), (False, False), (True, True)])
+def test_native_model_issues_the_python_models_calls(tmp_path, packed, split):
+    """model::PagedBatchModel (C++) and batch_model.PagedBatchModel (Python, GPU-tested) issue
+    the same libsq8 calls with the same arguments and buffer roles for the same steps, eagerly:
+    prefill-only, mixed and decode-only steps, fused and unfused epilogues, row-major or packed
+    weights, with and without the split-KV workspace. The C++ side runs under ASan/UBSan."""
+    steps = _script(np.random.default_rng(3))
+    py = _python_log(steps, packed, split)
+    cpp = _cpp_log(steps, packed, False, split, tmp_path)
+    assert len(cpp) == len(py)
+    for i, (a, b) in enumerate(zip(cpp, py)):
+        assert a == b, f"call {i}: C++ {a!r} != Python {b!r}"
+
+
+def test_native_model_graphs_replay_decode_steps(tmp_path):
+    """With graphs, the first decode-only step at a row count runs eagerly and is captured (its
+    launches appear twice); later decode-only steps at that count replay the graph; steps with
+    prefill rows always run eagerly. capture_decode_graphs() captures every count up front."""
+    steps = _script(np.random.default_rng(3))
+    eager = _cpp_log(steps, False, False, True, tmp_path)
+    log = _cpp_log(steps, False, True, True, tmp_path)
+    def per_step(lg):
+        counts = []
+        for line in lg:
+            if line == "step":
+                counts.append(0)
+            elif counts:
+                counts[-1] += 1
+        return counts
+    e, g = per_step(eager), per_step(log)
+    n = e[2]  # launches of one 5-row decode-only step
+    assert g[2] == 2 * n and g[3] == 1  # eager + capture, then one graph launch
+    assert g[0] == e[0] and g[1] == e[1]  # steps with prefill rows stay eager
+    log = _cpp_log(steps, False, True, True, tmp_path, capture_first=True)
+    g = per_step(log)
+    assert g[2] == 1 and g[3] == 1 and g[6] == 1 and g[8] == 1
