@@ -1,4 +1,4 @@
-/* Plain C interface to model::PagedBatchModel (libsq8_op.so). sq8_batch_model_forward has the
+/* Plain C interface to model::PagedBatchModel and model::Int8Decoder (libsq8_op.so). sq8_batch_model_forward has the
  * signature of sq8_sched_forward_fn (scheduler/scheduler_c.h), so a native scheduler can drive
  * the native model with no host language in between. No reference counterpart: the reference
  * calls its C++ model from C++ only. */
@@ -41,6 +41,22 @@ int sq8_batch_model_capture_decode_graphs(void* model);
 /* graph replays, rows run, captured graphs (as many as fit in n); returns the count written. */
 int sq8_batch_model_stats(void* model, int64_t* out, int n);
 const char* sq8_batch_model_last_error(void* model);
+
+/* model::Int8Decoder, the greedy single-sequence decoder (row-major weights, arguments as
+ * sq8_batch_model_create). generate: prompt tokens one step each, then n_new greedy tokens into
+ * out; use_graph: one HIP-graph replay per generated token. Returns 0, or non-zero with a
+ * message in sq8_decoder_last_error. */
+void* sq8_decoder_create(const sq8_model_config* cfg, const int8_t* const* qkv_q,
+                         const float* const* qkv_s, const int8_t* const* o_q,
+                         const float* const* o_s, const int8_t* const* gu_q,
+                         const float* const* gu_s, const int8_t* const* down_q,
+                         const float* const* down_s, const int8_t* cls_q, const float* cls_s,
+                         const float* embedding, const float* const* norm, int max_seq,
+                         int split_attention, void* hip_stream, const char** error);
+void sq8_decoder_destroy(void* decoder);
+int sq8_decoder_generate(void* decoder, const int32_t* prompt, int n_prompt, int n_new,
+                         int32_t* out, int use_graph);
+const char* sq8_decoder_last_error(void* decoder);
 
 #ifdef __cplusplus
 }

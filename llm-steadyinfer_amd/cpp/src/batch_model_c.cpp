@@ -1,10 +1,11 @@
-// C interface to model::PagedBatchModel (model/batch_model_c.h).
+// C interface to model::PagedBatchModel and model::Int8Decoder (model/batch_model_c.h).
 #include "model/batch_model_c.h"
 
 #include <algorithm>
 #include <memory>
 #include <string>
 
+#include "model/int8_decoder.h"
 #include "model/paged_batch_model.h"
 
 namespace {
@@ -25,6 +26,101 @@ int report(Handle* h, const base::Status& st) {
 }  // namespace
 
 extern "C" {
+
+}  // extern "C"
+
+namespace {
+
+bool fill(const sq8_model_config* cfg, const int8_t* const* qkv_q, const float* const* qkv_s,
+          const int8_t* const* o_q, const float* const* o_s, const int8_t* const* gu_q,
+          const float* const* gu_s, const int8_t* const* down_q, const float* const* down_s,
+          const int8_t* cls_q, const float* cls_s, const float* embedding,
+          const float* const* norm, model::BatchModelConfig* c, model::BatchModelWeights* w) {
+  if (!cfg || !qkv_q || !qkv_s || !o_q || !o_s || !gu_q || !gu_s || !down_q || !down_s ||
+      !norm || cfg->layer_num <= 0)
+    return false;
+  c->dim = cfg->dim;
+  c->hidden_dim = cfg->hidden_dim;
+  c->layer_num = cfg->layer_num;
+  c->head_num = cfg->head_num;
+  c->kv_head_num = cfg->kv_head_num;
+  c->vocab_size = cfg->vocab_size;
+  c->rope_theta = cfg->rope_theta;
+  c->group_size = cfg->group_size;
+  c->eps = cfg->eps;
+  for (int l = 0; l < c->layer_num; ++l) {
+    w->qkv.push_back({qkv_q[l], qkv_s[l]});
+    w->o.push_back({o_q[l], o_s[l]});
+    w->gu.push_back({gu_q[l], gu_s[l]});
+    w->down.push_back({down_q[l], down_s[l]});
+  }
+  for (int i = 0; i < 2 * c->layer_num + 1; ++i) w->norm.push_back(norm[i]);
+  w->cls = {cls_q, cls_s};
+  w->embedding = embedding;
+  return true;
+}
+
+const char* keep_message(const std::string& m) {
+  static thread_local std::string msg;
+  msg = m;
+  return msg.c_str();
+}
+
+struct DecoderHandle {
+  std::unique_ptr<model::Int8Decoder> dec;
+  std::string error;
+};
+
+}  // namespace
+
+extern "C" {
+
+void* sq8_decoder_create(const sq8_model_config* cfg, const int8_t* const* qkv_q,
+                         const float* const* qkv_s, const int8_t* const* o_q,
+                         const float* const* o_s, const int8_t* const* gu_q,
+                         const float* const* gu_s, const int8_t* const* down_q,
+                         const float* const* down_s, const int8_t* cls_q, const float* cls_s,
+                         const float* embedding, const float* const* norm, int max_seq,
+                         int split_attention, void* hip_stream, const char** error) {
+  model::BatchModelConfig c;
+  model::BatchModelWeights w;
+  if (!fill(cfg, qkv_q, qkv_s, o_q, o_s, gu_q, gu_s, down_q, down_s, cls_q, cls_s, embedding,
+            norm, &c, &w)) {
+    if (error) *error = "null argument or no layers";
+    return nullptr;
+  }
+  auto h = std::make_unique<DecoderHandle>();
+  h->dec = std::make_unique<model::Int8Decoder>(c, w, max_seq,
+                                                static_cast<hipStream_t>(hip_stream),
+                                                split_attention != 0);
+  const base::Status st = h->dec->init();
+  if (!st) {
+    if (error) *error = keep_message(st.get_err_msg());
+    return nullptr;
+  }
+  return h.release();
+}
+
+void sq8_decoder_destroy(void* decoder) { delete static_cast<DecoderHandle*>(decoder); }
+
+int sq8_decoder_generate(void* decoder, const int32_t* prompt, int n_prompt, int n_new,
+                         int32_t* out, int use_graph) {
+  if (!decoder || !prompt || n_prompt <= 0 || n_new < 0 || (n_new > 0 && !out)) return 1;
+  auto* h = static_cast<DecoderHandle*>(decoder);
+  std::vector<int32_t> toks;
+  const base::Status st = h->dec->generate(std::vector<int32_t>(prompt, prompt + n_prompt),
+                                           n_new, &toks, use_graph != 0);
+  if (!st) {
+    h->error = st.get_err_msg();
+    return 1;
+  }
+  std::copy(toks.begin(), toks.end(), out);
+  return 0;
+}
+
+const char* sq8_decoder_last_error(void* decoder) {
+  return decoder ? static_cast<DecoderHandle*>(decoder)->error.c_str() : "null decoder";
+}
 
 void* sq8_batch_model_create(const sq8_model_config* cfg, const int8_t* const* qkv_q,
                              const float* const* qkv_s, const int8_t* const* o_q,

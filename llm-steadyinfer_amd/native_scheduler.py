@@ -345,6 +345,45 @@ class NativePagedBatchModel:
                                    np.asarray(tables, np.int32).reshape(len(rows), -1), nd)
 
 
+class NativeInt8Decoder:
+    """model::Int8Decoder (C++, libsq8_op.so): the greedy single-sequence decoder of decoder.py
+    (fused step, one HIP-graph replay per token) over the same weight dict (row-major)."""
+
+    def __init__(self, cfg, weights: dict, group_size: int, max_seq: int,
+                 split_attention: bool = True, eps: float = 1e-6):
+        L = op_lib()
+        _bind_model(L)
+        self.w, self.cfg, self.max_seq = weights, cfg, max_seq
+        ptrs = lambda ts: (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
+        c = ModelConfigC(cfg.dim, cfg.hidden_dim, cfg.layer_num, cfg.head_num, cfg.kv_head_num,
+                         cfg.vocab, float(cfg.rope_theta), group_size, eps)
+        arrs = {k: (ptrs([q for q, _ in weights[k]]), ptrs([s for _, s in weights[k]]))
+                for k in ("qkv", "o", "gu", "down")}
+        err = ctypes.c_char_p()
+        self._h = L.sq8_decoder_create(
+            ctypes.byref(c), arrs["qkv"][0], arrs["qkv"][1], arrs["o"][0], arrs["o"][1],
+            arrs["gu"][0], arrs["gu"][1], arrs["down"][0], arrs["down"][1],
+            weights["cls"][0].data_ptr(), weights["cls"][1].data_ptr(),
+            weights["emb"].data_ptr(), ptrs(weights["norm"]), max_seq, int(split_attention),
+            None, ctypes.byref(err))
+        if not self._h:
+            raise RuntimeError("native decoder: " + (err.value or b"?").decode())
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            op_lib().sq8_decoder_destroy(h)
+            self._h = None
+
+    def generate(self, prompt, n_new: int, use_graph: bool = True):
+        arr, p = _i32(list(prompt))
+        out = (ctypes.c_int32 * max(n_new, 1))()
+        if op_lib().sq8_decoder_generate(self._h, p, len(arr), n_new, out, int(use_graph)):
+            raise RuntimeError("native decoder: " +
+                               op_lib().sq8_decoder_last_error(self._h).decode())
+        return list(out[:n_new])
+
+
 class ModelConfigC(ctypes.Structure):
     _fields_ = [("dim", ctypes.c_int), ("hidden_dim", ctypes.c_int),
                 ("layer_num", ctypes.c_int), ("head_num", ctypes.c_int),
@@ -355,7 +394,8 @@ class ModelConfigC(ctypes.Structure):
 
 MODEL_SYMBOLS = ("sq8_batch_model_create", "sq8_batch_model_destroy", "sq8_batch_model_forward",
                  "sq8_batch_model_capture_decode_graphs", "sq8_batch_model_stats",
-                 "sq8_batch_model_last_error")
+                 "sq8_batch_model_last_error", "sq8_decoder_create", "sq8_decoder_destroy",
+                 "sq8_decoder_generate", "sq8_decoder_last_error")
 _model_bound = False
 
 
@@ -377,4 +417,13 @@ def _bind_model(L):
     L.sq8_batch_model_stats.restype = I
     L.sq8_batch_model_last_error.argtypes = [vp]
     L.sq8_batch_model_last_error.restype = ctypes.c_char_p
+    L.sq8_decoder_create.argtypes = [ctypes.POINTER(ModelConfigC)] + [vp] * 12 + \
+        [I, I, vp, ctypes.POINTER(ctypes.c_char_p)]
+    L.sq8_decoder_create.restype = vp
+    L.sq8_decoder_destroy.argtypes = [vp]
+    L.sq8_decoder_destroy.restype = None
+    L.sq8_decoder_generate.argtypes = [vp, _P32, I, I, _P32, I]
+    L.sq8_decoder_generate.restype = I
+    L.sq8_decoder_last_error.argtypes = [vp]
+    L.sq8_decoder_last_error.restype = ctypes.c_char_p
     _model_bound = True

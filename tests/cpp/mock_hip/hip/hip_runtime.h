@@ -18,7 +18,7 @@ typedef int* hipEvent_t;
 typedef int* hipGraph_t;
 typedef int* hipGraphExec_t;
 typedef int* hipGraphNode_t;
-enum hipMemcpyKind { hipMemcpyHostToDevice = 1, hipMemcpyDeviceToHost = 2 };
+enum hipMemcpyKind { hipMemcpyHostToDevice = 1, hipMemcpyDeviceToHost = 2, hipMemcpyDeviceToDevice = 3 };
 enum hipStreamCaptureMode { hipStreamCaptureModeThreadLocal = 1 };
 enum { hipStreamNonBlocking = 1, hipEventDisableTiming = 2, hipHostMallocDefault = 0 };
 

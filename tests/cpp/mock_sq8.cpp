@@ -145,6 +145,45 @@ int sq8_swiglu_rows(const float* gu, int rows, int ffn, float* out, void*) {
   Line("sq8_swiglu_rows").p(gu).i(rows).i(ffn).p(out);
   return 0;
 }
+size_t sq8_workspace_bytes(int, int, int, int) { return 4096; }
+size_t sq8_argmax_workspace_bytes(int) { return 1024; }
+size_t sq8_decode_attention_workspace_bytes(int, int, int) { return 2048; }
+int sq8_matmul_rmsnorm(const float* x, const float* res, float* x_out, const float* nw, float eps,
+                       const int8_t* w, const float* s, float* y, int N, int K, int gs, void*) {
+  Line("sq8_matmul_rmsnorm").p(x).p(res).p(x_out).p(nw).f(eps).p(w).p(s).p(y).i(N).i(K).i(gs);
+  return 0;
+}
+int sq8_matmul_rmsnorm_swiglu(const float* x, const float* res, float* x_out, const float* nw,
+                              float eps, const int8_t* w, const float* s, float* y, int N, int K,
+                              int gs, void*) {
+  Line("sq8_matmul_rmsnorm_swiglu").p(x).p(res).p(x_out).p(nw).f(eps).p(w).p(s).p(y).i(N).i(K)
+      .i(gs);
+  return 0;
+}
+int sq8_rope_attention_decode(const float* qkv, int h, int kvh, int hs, const int32_t* pos,
+                              const float* sn, const float* cs, float* kc, float* vc, float* out,
+                              int max_seq, void*) {
+  Line("sq8_rope_attention_decode").p(qkv).i(h).i(kvh).i(hs).p(pos).p(sn).p(cs).p(kc).p(vc)
+      .p(out).i(max_seq);
+  return 0;
+}
+int sq8_rope_attention_decode_ws(const float* qkv, int h, int kvh, int hs, const int32_t* pos,
+                                 const float* sn, const float* cs, float* kc, float* vc,
+                                 float* out, int max_seq, void* ws, size_t wsb, void*) {
+  Line("sq8_rope_attention_decode_ws").p(qkv).i(h).i(kvh).i(hs).p(pos).p(sn).p(cs).p(kc).p(vc)
+      .p(out).i(max_seq).p(ws).i(wsb);
+  return 0;
+}
+int sq8_argmax_advance(const float* logits, int n, void* ws, size_t wsb, int32_t* pos,
+                       int32_t* token, const float* emb, int vocab, int dim, float* x, void*) {
+  Line("sq8_argmax_advance").p(logits).i(n).p(ws).i(wsb).p(pos).p(token).p(emb).i(vocab).i(dim)
+      .p(x);
+  return 0;
+}
+int sq8_step_advance(int32_t* pos, int32_t* token, const int32_t* next, void*) {
+  Line("sq8_step_advance").p(pos).p(token).p(next);
+  return 0;
+}
 int sq8_argmax_rows(const float* logits, int rows, int n, int32_t* out, void*) {
   Line("sq8_argmax_rows").p(logits).i(rows).i(n).p(out);
   return 0;

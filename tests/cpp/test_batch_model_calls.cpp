@@ -1,26 +1,31 @@
-// Prints the libsq8 calls model::PagedBatchModel issues for a scripted sequence of steps, built
+// Prints the libsq8 calls model::PagedBatchModel (or, in decoder mode, model::Int8Decoder) issues
+// for a scripted run, built
 // with g++ against host stand-ins of the HIP runtime (tests/cpp/mock_hip) and of libsq8
 // (tests/cpp/mock_sq8.cpp). tests/test_native_scheduler.py compares the log with the calls the
 // Python PagedBatchModel issues for the same steps.
 //
-// stdin: "packed use_graphs split_kv", then per step "B nd", B tokens, B positions and
+// stdin, batch mode: "batch packed use_graphs split_kv", then per step "B nd", B tokens, B positions and
 // B * table_stride block-table entries; "capture" instead of a step calls
 // capture_decode_graphs(). Model: dim 64, FFN 96, 2 layers, 4 / 2 heads, vocab 50, 8 rows,
-// max_seq 64, 40 blocks of 4.
+// max_seq 64, 40 blocks of 4. Decoder mode: "decoder use_graph split n_new n_prompt" and the
+// prompt tokens (same model, max_seq 64).
 #include <cstdio>
 #include <cstdlib>
 #include <iostream>
 #include <string>
 #include <vector>
 
+#include "model/int8_decoder.h"
 #include "model/paged_batch_model.h"
 
 void mock_print_log();
 void mock_mark(const char* what);
 
 int main() {
+  std::string mode;
   int packed = 0, graphs = 0, split = 0;
-  if (!(std::cin >> packed >> graphs >> split)) return 2;
+  if (!(std::cin >> mode)) return 2;
+  if (mode == "batch" && !(std::cin >> packed >> graphs >> split)) return 2;
   model::BatchModelConfig c;
   c.dim = 64;
   c.hidden_dim = 96;
@@ -44,6 +49,22 @@ int main() {
   w.embedding = static_cast<const float*>(fake());
   for (int i = 0; i < 2 * c.layer_num + 1; ++i) w.norm.push_back(static_cast<const float*>(fake()));
   w.packed = packed != 0;
+  if (mode == "decoder") {
+    int use_graph = 0, n_new = 0, np = 0;
+    std::cin >> use_graph >> split >> n_new >> np;
+    std::vector<int32_t> prompt(np), out;
+    for (auto& t : prompt) std::cin >> t;
+    model::Int8Decoder dec(c, w, 64, nullptr, split != 0);
+    base::Status st = dec.init();
+    if (st) st = dec.generate(prompt, n_new, &out, use_graph != 0);
+    if (!st) {
+      std::printf("decoder failed: %s\n", st.get_err_msg().c_str());
+      return 1;
+    }
+    mock_print_log();
+    for (void* p : bufs) std::free(p);
+    return 0;
+  }
   model::PagedBatchModel m(c, w, 8, 64, 40, 4, nullptr, graphs != 0, split != 0);
   base::Status st = m.init();
   if (!st) {

@@ -229,6 +229,12 @@ def test_native_scheduler_calls_a_native_forward_directly():
 # Argument kinds of the logged libsq8 calls, in C order: p pointer, i integer, f float, s stream
 # (not logged). Workspace sizes and the fused-epilogue rule restate tests/cpp/mock_sq8.cpp.
 _SPEC = {
+    "sq8_matmul_rmsnorm": "ppppfpppiiis",
+    "sq8_matmul_rmsnorm_swiglu": "ppppfpppiiis",
+    "sq8_rope_attention_decode": "piiippppppis",
+    "sq8_rope_attention_decode_ws": "piiippppppipis",
+    "sq8_argmax_advance": "pipipppiips",
+    "sq8_step_advance": "ppps",
     "sq8_matmul": "ppppiiiipis", "sq8_matmul_packed": "ppppiiiipis",
     "sq8_matmul_epilogue": "ppppiiiiippis", "sq8_matmul_epilogue_packed": "ppppiiiiippis",
     "sq8_matmul_rmsnorm_rows": "pppfpppiiiiipis", "sq8_matmul_rmsnorm_rows_packed":
@@ -272,6 +278,10 @@ class _RecordingLib:
             return lambda *a: 8192
         if name == "sq8_workspace_bytes":
             return lambda *a: 4096
+        if name == "sq8_argmax_workspace_bytes":
+            return lambda *a: 1024
+        if name == "sq8_decode_attention_workspace_bytes":
+            return lambda *a: 2048
         if name == "sq8_paged_attention_workspace_bytes":
             return lambda *a: 2048
         if name == "sq8_packed_weight_bytes":
@@ -332,23 +342,38 @@ def _python_log(steps, packed, split):
     return rec.log
 
 
-def _cpp_log(steps, packed, graphs, split, tmp_path, capture_first=False):
+_EXE = {}
+
+
+def _calls_exe(tmp_path):
+    """The call-log program, compiled once per test session."""
     import shutil
     import subprocess
     from conftest import REPO
     if shutil.which("g++") is None:
         pytest.skip("g++ not available")
+    if "calls" in _EXE and _EXE["calls"].exists():
+        return _EXE["calls"]
     exe = tmp_path / "test_batch_model_calls"
+    _EXE["calls"] = exe
     if not exe.exists():
         cpp = REPO / "llm-steadyinfer_amd" / "cpp"
         t = REPO / "tests" / "cpp"
         cmd = ["g++", "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined",
                "-fno-sanitize-recover=undefined", "-I", str(t / "mock_hip"), "-I",
                str(cpp / "include"), "-I", str(t), str(t / "test_batch_model_calls.cpp"),
-               str(t / "mock_sq8.cpp"), str(cpp / "src" / "paged_batch_model.cpp"), "-o", str(exe)]
+               str(t / "mock_sq8.cpp"), str(cpp / "src" / "paged_batch_model.cpp"),
+               str(cpp / "src" / "int8_decoder.cpp"), "-o", str(exe)]
         res = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
         assert res.returncode == 0, res.stderr[-3000:]
-    lines = [f"{int(packed)} {int(graphs)} {int(split)}"] + (["capture"] if capture_first else [])
+    return exe
+
+
+def _cpp_log(steps, packed, graphs, split, tmp_path, capture_first=False):
+    import subprocess
+    exe = _calls_exe(tmp_path)
+    lines = [f"batch {int(packed)} {int(graphs)} {int(split)}"] + \
+        (["capture"] if capture_first else [])
     for B, nd, rows in steps:
         lines.append(f"{B} {nd}")
         lines.append(" ".join(str(r[0]) for r in rows))
@@ -396,3 +421,71 @@ def test_native_model_graphs_replay_decode_steps(tmp_path):
     log = _cpp_log(steps, False, True, True, tmp_path, capture_first=True)
     g = per_step(log)
     assert g[2] == 1 and g[3] == 1 and g[6] == 1 and g[8] == 1
+
+
+def _python_decoder_log(prompt, n_new, split):
+    import torch
+    pkg = load_pkg()
+    dec = importlib.import_module("llm_steadyinfer_amd.decoder")
+    mf = importlib.import_module("llm_steadyinfer_amd.model_file")
+    rec = _RecordingLib()
+    saved = (pkg.lib, dec.lib, torch.cuda.current_stream, torch.cuda.synchronize)
+
+    class _S:
+        cuda_stream = 0
+    try:
+        pkg.lib = dec.lib = lambda: rec
+        torch.cuda.current_stream = lambda *a, **k: _S()
+        torch.cuda.synchronize = lambda *a, **k: None
+        pkg._check_matmul_saved = pkg._check_matmul
+        pkg._check_matmul = lambda *a, **k: None
+        cfg = mf.ModelConfig(dim=64, hidden_dim=96, layer_num=2, head_num=4, kv_head_num=2,
+                             vocab_size=-50, seq_len=64, rope_theta=1e6)
+        q = lambda n, k: (torch.zeros((n, k), dtype=torch.int8), torch.zeros(n * k // 64))
+        w = {"qkv": [q(128, 64) for _ in range(2)], "o": [q(64, 64) for _ in range(2)],
+             "gu": [q(192, 64) for _ in range(2)], "down": [q(64, 96) for _ in range(2)],
+             "cls": q(50, 64), "emb": torch.zeros((50, 64)),
+             "norm": [torch.ones(64) for _ in range(5)]}
+        d = dec.Int8Decoder(cfg, w, 64, 64, device="cpu")
+        if not split:
+            d.att_ws = None
+        d.generate(prompt, n_new, use_graph=False)
+    finally:
+        pkg._check_matmul = pkg._check_matmul_saved
+        pkg.lib, dec.lib, torch.cuda.current_stream, torch.cuda.synchronize = saved
+    return rec.log
+
+
+def _cpp_decoder_log(prompt, n_new, graph, split, tmp_path):
+    import subprocess
+    exe = _calls_exe(tmp_path)
+    inp = f"decoder {int(graph)} {int(split)} {n_new} {len(prompt)}\n" + \
+        " ".join(map(str, prompt)) + "\n"
+    res = subprocess.run([str(exe)], input=inp, capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-3000:]
+    return res.stdout.splitlines()
+
+
+@pytest.mark.parametrize("split", [True, False])
+def test_native_decoder_issues_the_python_decoders_calls(tmp_path, split):
+    """model::Int8Decoder (C++) and decoder.Int8Decoder (Python, GPU-tested) issue the same
+    libsq8 calls for a 5-token prompt and 4 generated tokens (eager steps): the fused QKV / gate
+    / up prologues with the residual stream ping-ponging, RoPE + attention in one launch, the
+    classifier and argmax + advance + embedding, and the prompt steps' embedding and advance."""
+    prompt = [3, 1, 4, 1, 5]
+    py = _python_decoder_log(prompt, 4, split)
+    cpp = _cpp_decoder_log(prompt, 4, False, split, tmp_path)
+    assert len(cpp) == len(py)
+    for i, (a, b) in enumerate(zip(cpp, py)):
+        assert a == b, f"call {i}: C++ {a!r} != Python {b!r}"
+
+
+def test_native_decoder_replays_one_graph_per_token(tmp_path):
+    """With the graph: the prompt steps run eagerly, one step is captured (its launches logged
+    once, not run), and each generated token is one graph launch."""
+    eager = _cpp_decoder_log([3, 1, 4], 5, False, True, tmp_path)
+    graph = _cpp_decoder_log([3, 1, 4], 5, True, True, tmp_path)
+    assert graph.count("graph_launch") == 5
+    steps_eager = sum(1 for l in eager if l.startswith("sq8_argmax_advance"))
+    steps_graph = sum(1 for l in graph if l.startswith("sq8_argmax_advance"))
+    assert steps_eager == 5 and steps_graph == 1
