@@ -119,3 +119,18 @@ def test_epilogue_fusion_and_workspace(sq8):
             # the product never lands in the 64 KiB ticket area of MFMA workspaces
             off = (max(base, 65536) + 255) // 256 * 256
             assert extra == (0 if sq8.epilogue_fused(M, N, K) else off + M * N * 4 - base)
+
+
+def test_op_library_exports_its_c_interfaces(sq8):
+    """libsq8_op.so exports every function of the scheduler and model C interfaces
+    (llm-steadyinfer_amd/cpp/include/scheduler/scheduler_c.h, model/batch_model_c.h), and the
+    Python binding binds exactly those."""
+    import importlib
+    nat = importlib.import_module("llm_steadyinfer_amd.native_scheduler")
+    inc = REPO / "llm-steadyinfer_amd" / "cpp" / "include"
+    sched_h, model_h = inc / "scheduler" / "scheduler_c.h", inc / "model" / "batch_model_c.h"
+    assert declared_functions((sched_h,)) == sorted(nat.SCHED_SYMBOLS)
+    assert declared_functions((model_h,)) == sorted(nat.MODEL_SYMBOLS)
+    lib = nat.op_lib()
+    for name in declared_functions((sched_h, model_h)):
+        assert hasattr(lib, name), name
