@@ -22,12 +22,20 @@ enum hipMemcpyKind { hipMemcpyHostToDevice = 1, hipMemcpyDeviceToHost = 2, hipMe
 enum hipStreamCaptureMode { hipStreamCaptureModeThreadLocal = 1 };
 enum { hipStreamNonBlocking = 1, hipEventDisableTiming = 2, hipHostMallocDefault = 0 };
 
+// Every allocation is registered (mock_sq8.cpp) so that logged pointers read as (allocation,
+// byte offset) and allocation sizes can be compared.
+void mock_register(const void* p, size_t bytes, int owned);
 inline const char* hipGetErrorString(hipError_t e) { return e ? "mock error" : "no error"; }
 inline hipError_t hipMalloc(void** p, size_t n) {
   *p = std::calloc(n, 1);
+  if (*p) mock_register(*p, n, 1);
   return *p ? hipSuccess : hipErrorOutOfMemory;
 }
-inline hipError_t hipHostMalloc(void** p, size_t n, unsigned) { return hipMalloc(p, n); }
+inline hipError_t hipHostMalloc(void** p, size_t n, unsigned) {
+  *p = std::calloc(n, 1);
+  if (*p) mock_register(*p, n, 0);  // pinned host staging: not a device buffer of the model
+  return *p ? hipSuccess : hipErrorOutOfMemory;
+}
 inline hipError_t hipFree(void* p) {
   std::free(p);
   return hipSuccess;

@@ -4,7 +4,9 @@
 // use their buffers in the same roles print the same log) and without the stream argument.
 // Workspace queries return fixed sizes and the fused-epilogue queries a fixed rule (fused when
 // M > 4 and N is even), restated by tests/test_native_scheduler.py for the Python model.
+#include <cstdint>
 #include <cstdio>
+#include <iterator>
 #include <map>
 #include <sstream>
 #include <string>
@@ -16,20 +18,34 @@
 #include "hip/hip_runtime.h"
 
 namespace {
-std::map<const void*, int> g_ids;
+struct Alloc {
+  size_t bytes;
+  int owned;  // allocated by the code under test (hipMalloc), not handed in
+  int id;     // order of first appearance in the log, 0 = not yet
+};
+std::map<uintptr_t, Alloc> g_allocs;
+int g_next_id = 0;
 std::vector<std::string> g_log;
 
 struct Line {
   std::ostringstream os;
   explicit Line(const char* name) { os << name; }
+  // A pointer as p<allocation id>[+<byte offset>]; "?" outside every registered allocation.
   Line& p(const void* v) {
     if (!v) {
       os << " 0";
-    } else {
-      auto it = g_ids.find(v);
-      if (it == g_ids.end()) it = g_ids.emplace(v, static_cast<int>(g_ids.size()) + 1).first;
-      os << " p" << it->second;
+      return *this;
     }
+    const uintptr_t a = reinterpret_cast<uintptr_t>(v);
+    auto it = g_allocs.upper_bound(a);
+    if (it == g_allocs.begin() || a >= std::prev(it)->first + std::prev(it)->second.bytes) {
+      os << " ?";
+      return *this;
+    }
+    --it;
+    if (it->second.id == 0) it->second.id = ++g_next_id;
+    os << " p" << it->second.id;
+    if (a != it->first) os << "+" << (a - it->first);
     return *this;
   }
   Line& i(long long v) {
@@ -50,8 +66,17 @@ hipError_t hipGraphLaunch(hipGraphExec_t, hipStream_t) {
   Line("graph_launch");
   return hipSuccess;
 }
+void mock_register(const void* p, size_t bytes, int owned) {
+  g_allocs[reinterpret_cast<uintptr_t>(p)] = Alloc{bytes, owned, 0};
+}
+// The log, then "alloc p<id> <bytes>" for every allocation of the code under test that the
+// log names, in id order.
 void mock_print_log() {
   for (const std::string& s : g_log) std::printf("%s\n", s.c_str());
+  std::map<int, size_t> sizes;
+  for (const auto& a : g_allocs)
+    if (a.second.owned && a.second.id) sizes[a.second.id] = a.second.bytes;
+  for (const auto& s : sizes) std::printf("alloc p%d %zu\n", s.first, s.second);
 }
 void mock_mark(const char* what) { Line l(what); }
 

@@ -20,6 +20,7 @@
 
 void mock_print_log();
 void mock_mark(const char* what);
+void mock_register(const void* p, size_t bytes, int owned);
 
 int main() {
   std::string mode;
@@ -36,8 +37,9 @@ int main() {
   c.rope_theta = 1e6f;
   c.group_size = 64;
   std::vector<void*> bufs;
-  auto fake = [&]() {
+  auto fake = [&]() {  // a weight buffer handed in by the caller (not the model's own)
     bufs.push_back(std::malloc(64));
+    mock_register(bufs.back(), 64, 0);
     return bufs.back();
   };
   model::BatchModelWeights w;

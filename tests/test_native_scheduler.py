@@ -246,8 +246,33 @@ _SPEC = {
 
 
 class _RecordingLib:
+    """Logs libsq8 calls like tests/cpp/mock_sq8.cpp: a pointer as p<allocation id>[+<byte
+    offset>], the allocation found among the tensors `sources()` returns as (tensor, owned)."""
+
     def __init__(self):
-        self.log, self.ids = [], {}
+        self.log, self.ids, self.sources, self.allocs = [], {}, (lambda: []), []
+
+    def _rescan(self):
+        seen = {}
+        for t, owned in self.sources():
+            st = t.untyped_storage()
+            seen[st.data_ptr()] = (st.nbytes(), owned)
+        self.allocs = sorted((b, n, o) for b, (n, o) in seen.items())
+
+    def _ptr(self, a):
+        for attempt in range(2):
+            for base, n, owned in self.allocs:
+                if base <= a < base + n:
+                    key = base
+                    if key not in self.ids:
+                        self.ids[key] = (len(self.ids) + 1, n, owned)
+                    i = self.ids[key][0]
+                    return f"p{i}" if a == base else f"p{i}+{a - base}"
+            self._rescan()
+        return "?"
+
+    def alloc_lines(self):
+        return [f"alloc p{i} {n}" for i, n, owned in sorted(self.ids.values()) if owned]
 
     def _fmt(self, name, args):
         out = [name]
@@ -258,7 +283,7 @@ class _RecordingLib:
                 if not a:
                     out.append("0")
                 else:
-                    out.append("p%d" % self.ids.setdefault(int(a), len(self.ids) + 1))
+                    out.append(self._ptr(int(a)))
             elif kind == "f":
                 out.append("%.6g" % np.float32(a))
             else:
@@ -289,6 +314,29 @@ class _RecordingLib:
         if name == "sq8_pack_weights":
             return lambda *a: 0
         raise AttributeError(name)
+
+
+def _tensors(model, weights):
+    """(tensor, owned) for the model's own buffers (attributes, workspaces) and the weights."""
+    import torch
+    out = []
+    if model is not None:
+        for v in list(vars(model).values()):
+            for t in (v, getattr(v, "buf", None)):
+                if isinstance(t, torch.Tensor):
+                    out.append((t, True))
+        for v in getattr(model, "w", {}).values():
+            items = v if isinstance(v, (list, tuple)) else [v]
+            for it in items:
+                for t in (it if isinstance(it, tuple) else (it,)):
+                    t = getattr(t, "data", t) if not isinstance(t, torch.Tensor) else t
+                    if isinstance(t, torch.Tensor):
+                        out.append((t, False))
+    for v in weights.values():
+        for it in (v if isinstance(v, list) else [v]):
+            for t in (it if isinstance(it, tuple) else (it,)):
+                out.append((t, False))
+    return out
 
 
 def _script(rng):
@@ -329,9 +377,11 @@ def _python_log(steps, packed, split):
              "gu": [q(192, 64) for _ in range(2)], "down": [q(64, 96) for _ in range(2)],
              "cls": q(50, 64), "emb": torch.zeros((50, 64)),
              "norm": [torch.ones(64) for _ in range(5)]}
-        m = bm.PagedBatchModel(cfg, w, 64, max_rows=8, max_seq_len=64, num_blocks=40,
-                               block_size=4, device="cpu", use_graphs=False, split_kv=split,
-                               packed=packed)
+        holder = {}
+        rec.sources = lambda: _tensors(holder.get("m"), w)
+        m = holder["m"] = bm.PagedBatchModel.__new__(bm.PagedBatchModel)
+        m.__init__(cfg, w, 64, max_rows=8, max_seq_len=64, num_blocks=40, block_size=4,
+                   device="cpu", use_graphs=False, split_kv=split, packed=packed)
         for B, nd, rows in steps:
             rec.log.append("step")
             m.forward_arrays(np.array([r[0] for r in rows], np.int32),
@@ -339,7 +389,7 @@ def _python_log(steps, packed, split):
                              np.array([r[2] for r in rows], np.int32), nd)
     finally:
         pkg.lib, bm.lib, pkg._check_matmul, pkg._check_paged, torch.cuda.current_stream = saved
-    return rec.log
+    return rec.log + rec.alloc_lines()
 
 
 _EXE = {}
@@ -446,14 +496,17 @@ def _python_decoder_log(prompt, n_new, split):
              "gu": [q(192, 64) for _ in range(2)], "down": [q(64, 96) for _ in range(2)],
              "cls": q(50, 64), "emb": torch.zeros((50, 64)),
              "norm": [torch.ones(64) for _ in range(5)]}
-        d = dec.Int8Decoder(cfg, w, 64, 64, device="cpu")
+        holder = {}
+        rec.sources = lambda: _tensors(holder.get("m"), w)
+        d = holder["m"] = dec.Int8Decoder.__new__(dec.Int8Decoder)
+        d.__init__(cfg, w, 64, 64, device="cpu")
         if not split:
             d.att_ws = None
         d.generate(prompt, n_new, use_graph=False)
     finally:
         pkg._check_matmul = pkg._check_matmul_saved
         pkg.lib, dec.lib, torch.cuda.current_stream, torch.cuda.synchronize = saved
-    return rec.log
+    return rec.log + rec.alloc_lines()
 
 
 def _cpp_decoder_log(prompt, n_new, graph, split, tmp_path):
