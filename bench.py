@@ -285,7 +285,7 @@ def copy_ceiling(torch, dev, shapes):
 
 
 def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed: int = 0,
-              sigma: float = 0.8, packed: bool = False, native: bool = True,
+              sigma: float = 0.8, packed: bool = False, native: bool = False,
               native_model: bool = False):
     """Config 5: continuous batching of n_seqs requests on the Llama-3-8B-shaped INT8 model (the
     step's random-init projections, plus a random embedding and unit norms). Prompt lengths are
@@ -379,10 +379,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-batch", action="store_true", help="skip config 5 (continuous batching)")
-    ap.add_argument("--py-scheduler", action="store_true",
-                    help="config 5 on the Python scheduler (default: the C++ scheduler)")
+    ap.add_argument("--native-scheduler", action="store_true",
+                    help="config 5 on the C++ scheduler (scheduler::Scheduler) instead of the "
+                         "Python one")
     ap.add_argument("--native-model", action="store_true",
-                    help="config 5 on the C++ batch model as well (no Python in the step loop)")
+                    help="config 5 on the C++ scheduler and the C++ batch model (no Python in "
+                         "the step loop)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--graph", action="store_true", help="replay the step as one HIP graph")
     ap.add_argument("--profile", action="store_true",
@@ -634,14 +636,14 @@ def main():
 
     batch = None
     if not args.no_batch:
-        batch = batch_run(torch, weights, lm_head, native=not args.py_scheduler,
+        batch = batch_run(torch, weights, lm_head, native=args.native_scheduler,
                           native_model=args.native_model)
         print(f"# batch done: {batch['output_tokens_per_s']} output tokens/s", file=sys.stderr,
               flush=True)
     batch_packed = None
     if args.packed and not args.no_batch:
         batch_packed = batch_run(torch, weights, lm_head, packed=True,
-                                 native=not args.py_scheduler,
+                                 native=args.native_scheduler,
                                  native_model=args.native_model)
         print(f"# packed batch done: {batch_packed['output_tokens_per_s']} output tokens/s",
               file=sys.stderr, flush=True)
