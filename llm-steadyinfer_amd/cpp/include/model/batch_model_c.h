@@ -58,6 +58,15 @@ int sq8_decoder_generate(void* decoder, const int32_t* prompt, int n_prompt, int
                          int32_t* out, int use_graph);
 const char* sq8_decoder_last_error(void* decoder);
 
+/* The same models from an INT8 model file (the reference's .bin layout), read by the C++ loader
+ * (model::Int8ModelFile) and uploaded fused (model::DeviceWeights); the handle owns the device
+ * weights. Destroy with sq8_batch_model_destroy / sq8_decoder_destroy. */
+void* sq8_batch_model_create_from_file(const char* path, int packed, int max_rows,
+                                       int max_seq_len, int num_blocks, int block_size,
+                                       int use_graphs, int split_kv, const char** error);
+void* sq8_decoder_create_from_file(const char* path, int max_seq, int split_attention,
+                                   const char** error);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,12 +5,14 @@
 #include <memory>
 #include <string>
 
+#include "model/device_weights.h"
 #include "model/int8_decoder.h"
 #include "model/paged_batch_model.h"
 
 namespace {
 
 struct Handle {
+  std::unique_ptr<model::DeviceWeights> weights;  // when created from a file (outlives model)
   std::unique_ptr<model::PagedBatchModel> model;
   std::string error;
 };
@@ -22,14 +24,6 @@ int report(Handle* h, const base::Status& st) {
   h->error = st.get_err_msg();
   return 1;
 }
-
-}  // namespace
-
-extern "C" {
-
-}  // extern "C"
-
-namespace {
 
 bool fill(const sq8_model_config* cfg, const int8_t* const* qkv_q, const float* const* qkv_s,
           const int8_t* const* o_q, const float* const* o_s, const int8_t* const* gu_q,
@@ -67,9 +61,27 @@ const char* keep_message(const std::string& m) {
 }
 
 struct DecoderHandle {
+  std::unique_ptr<model::DeviceWeights> weights;  // when created from a file (outlives dec)
   std::unique_ptr<model::Int8Decoder> dec;
   std::string error;
 };
+
+// Reads and uploads a model file; nullptr with *error set on failure.
+std::unique_ptr<model::DeviceWeights> load(const char* path, bool packed, const char** error) {
+  if (!path) {
+    if (error) *error = "null path";
+    return nullptr;
+  }
+  model::Int8ModelFile file;
+  base::Status st = file.open(path);
+  auto w = std::make_unique<model::DeviceWeights>();
+  if (st) st = w->upload(file, packed);
+  if (!st) {
+    if (error) *error = keep_message(st.get_err_msg());
+    return nullptr;
+  }
+  return w;
+}
 
 }  // namespace
 
@@ -94,6 +106,39 @@ void* sq8_decoder_create(const sq8_model_config* cfg, const int8_t* const* qkv_q
                                                 static_cast<hipStream_t>(hip_stream),
                                                 split_attention != 0);
   const base::Status st = h->dec->init();
+  if (!st) {
+    if (error) *error = keep_message(st.get_err_msg());
+    return nullptr;
+  }
+  return h.release();
+}
+
+void* sq8_decoder_create_from_file(const char* path, int max_seq, int split_attention,
+                                   const char** error) {
+  auto h = std::make_unique<DecoderHandle>();
+  h->weights = load(path, false, error);
+  if (!h->weights) return nullptr;
+  model::BatchModelConfig c = h->weights->config();
+  h->dec = std::make_unique<model::Int8Decoder>(c, h->weights->weights(), max_seq, nullptr,
+                                                split_attention != 0);
+  const base::Status st = h->dec->init();
+  if (!st) {
+    if (error) *error = keep_message(st.get_err_msg());
+    return nullptr;
+  }
+  return h.release();
+}
+
+void* sq8_batch_model_create_from_file(const char* path, int packed, int max_rows,
+                                       int max_seq_len, int num_blocks, int block_size,
+                                       int use_graphs, int split_kv, const char** error) {
+  auto h = std::make_unique<Handle>();
+  h->weights = load(path, packed != 0, error);
+  if (!h->weights) return nullptr;
+  h->model = std::make_unique<model::PagedBatchModel>(
+      h->weights->config(), h->weights->weights(), max_rows, max_seq_len, num_blocks, block_size,
+      nullptr, use_graphs != 0, split_kv != 0);
+  const base::Status st = h->model->init();
   if (!st) {
     if (error) *error = keep_message(st.get_err_msg());
     return nullptr;
@@ -131,33 +176,13 @@ void* sq8_batch_model_create(const sq8_model_config* cfg, const int8_t* const* q
                              const float* const* norm, int packed, int max_rows, int max_seq_len,
                              int num_blocks, int block_size, int use_graphs, int split_kv,
                              void* hip_stream, const char** error) {
-  auto fail = [&](const char* why) -> void* {
-    if (error) *error = why;
-    return nullptr;
-  };
-  if (!cfg || !qkv_q || !qkv_s || !o_q || !o_s || !gu_q || !gu_s || !down_q || !down_s || !norm)
-    return fail("null argument");
-  if (cfg->layer_num <= 0) return fail("layer_num must be positive");
   model::BatchModelConfig c;
-  c.dim = cfg->dim;
-  c.hidden_dim = cfg->hidden_dim;
-  c.layer_num = cfg->layer_num;
-  c.head_num = cfg->head_num;
-  c.kv_head_num = cfg->kv_head_num;
-  c.vocab_size = cfg->vocab_size;
-  c.rope_theta = cfg->rope_theta;
-  c.group_size = cfg->group_size;
-  c.eps = cfg->eps;
   model::BatchModelWeights w;
-  for (int l = 0; l < c.layer_num; ++l) {
-    w.qkv.push_back({qkv_q[l], qkv_s[l]});
-    w.o.push_back({o_q[l], o_s[l]});
-    w.gu.push_back({gu_q[l], gu_s[l]});
-    w.down.push_back({down_q[l], down_s[l]});
+  if (!fill(cfg, qkv_q, qkv_s, o_q, o_s, gu_q, gu_s, down_q, down_s, cls_q, cls_s, embedding,
+            norm, &c, &w)) {
+    if (error) *error = "null argument or no layers";
+    return nullptr;
   }
-  for (int i = 0; i < 2 * c.layer_num + 1; ++i) w.norm.push_back(norm[i]);
-  w.cls = {cls_q, cls_s};
-  w.embedding = embedding;
   w.packed = packed != 0;
   auto h = std::make_unique<Handle>();
   h->model = std::make_unique<model::PagedBatchModel>(
@@ -165,9 +190,8 @@ void* sq8_batch_model_create(const sq8_model_config* cfg, const int8_t* const* q
       use_graphs != 0, split_kv != 0);
   const base::Status st = h->model->init();
   if (!st) {
-    static thread_local std::string msg;
-    msg = st.get_err_msg();
-    return fail(msg.c_str());
+    if (error) *error = keep_message(st.get_err_msg());
+    return nullptr;
   }
   return h.release();
 }

@@ -296,6 +296,27 @@ class NativePagedBatchModel:
         self.native_forward = (ctypes.cast(L.sq8_batch_model_forward, ctypes.c_void_p).value,
                                self._h)
 
+    @classmethod
+    def from_file(cls, path, max_rows: int, max_seq_len: int, num_blocks: int, block_size: int,
+                  use_graphs: bool = True, split_kv: bool = True, packed: bool = False):
+        """The model from an INT8 model file, read and uploaded in C++ (model::Int8ModelFile,
+        model::DeviceWeights); no Python touches the weights."""
+        L = op_lib()
+        _bind_model(L)
+        self = cls.__new__(cls)
+        self.w = None
+        self.max_rows, self.block_size = max_rows, block_size
+        self.max_blocks_per_seq = (max_seq_len + block_size - 1) // block_size
+        err = ctypes.c_char_p()
+        self._h = L.sq8_batch_model_create_from_file(
+            str(path).encode(), int(packed), max_rows, max_seq_len, num_blocks, block_size,
+            int(use_graphs), int(split_kv), ctypes.byref(err))
+        if not self._h:
+            raise RuntimeError("native batch model: " + (err.value or b"?").decode())
+        self.native_forward = (ctypes.cast(L.sq8_batch_model_forward, ctypes.c_void_p).value,
+                               self._h)
+        return self
+
     def __del__(self):
         h = getattr(self, "_h", None)
         if h:
@@ -369,6 +390,20 @@ class NativeInt8Decoder:
         if not self._h:
             raise RuntimeError("native decoder: " + (err.value or b"?").decode())
 
+    @classmethod
+    def from_file(cls, path, max_seq: int, split_attention: bool = True):
+        """The decoder from an INT8 model file, read and uploaded in C++."""
+        L = op_lib()
+        _bind_model(L)
+        self = cls.__new__(cls)
+        self.w, self.cfg, self.max_seq = None, None, max_seq
+        err = ctypes.c_char_p()
+        self._h = L.sq8_decoder_create_from_file(str(path).encode(), max_seq,
+                                                 int(split_attention), ctypes.byref(err))
+        if not self._h:
+            raise RuntimeError("native decoder: " + (err.value or b"?").decode())
+        return self
+
     def __del__(self):
         h = getattr(self, "_h", None)
         if h:
@@ -395,7 +430,8 @@ class ModelConfigC(ctypes.Structure):
 MODEL_SYMBOLS = ("sq8_batch_model_create", "sq8_batch_model_destroy", "sq8_batch_model_forward",
                  "sq8_batch_model_capture_decode_graphs", "sq8_batch_model_stats",
                  "sq8_batch_model_last_error", "sq8_decoder_create", "sq8_decoder_destroy",
-                 "sq8_decoder_generate", "sq8_decoder_last_error")
+                 "sq8_decoder_generate", "sq8_decoder_last_error",
+                 "sq8_batch_model_create_from_file", "sq8_decoder_create_from_file")
 _model_bound = False
 
 
@@ -426,4 +462,10 @@ def _bind_model(L):
     L.sq8_decoder_generate.restype = I
     L.sq8_decoder_last_error.argtypes = [vp]
     L.sq8_decoder_last_error.restype = ctypes.c_char_p
+    L.sq8_batch_model_create_from_file.argtypes = [ctypes.c_char_p, I, I, I, I, I, I, I,
+                                                   ctypes.POINTER(ctypes.c_char_p)]
+    L.sq8_batch_model_create_from_file.restype = vp
+    L.sq8_decoder_create_from_file.argtypes = [ctypes.c_char_p, I, I,
+                                               ctypes.POINTER(ctypes.c_char_p)]
+    L.sq8_decoder_create_from_file.restype = vp
     _model_bound = True

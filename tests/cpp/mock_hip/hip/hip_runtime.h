@@ -18,7 +18,13 @@ typedef int* hipEvent_t;
 typedef int* hipGraph_t;
 typedef int* hipGraphExec_t;
 typedef int* hipGraphNode_t;
-enum hipMemcpyKind { hipMemcpyHostToDevice = 1, hipMemcpyDeviceToHost = 2, hipMemcpyDeviceToDevice = 3 };
+enum hipMemcpyKind {
+  hipMemcpyHostToHost = 0,
+  hipMemcpyHostToDevice = 1,
+  hipMemcpyDeviceToHost = 2,
+  hipMemcpyDeviceToDevice = 3
+};
+enum hipStreamCaptureStatus { hipStreamCaptureStatusNone = 0, hipStreamCaptureStatusActive = 1 };
 enum hipStreamCaptureMode { hipStreamCaptureModeThreadLocal = 1 };
 enum { hipStreamNonBlocking = 1, hipEventDisableTiming = 2, hipHostMallocDefault = 0 };
 
@@ -52,7 +58,21 @@ inline hipError_t hipMemcpyAsync(void* d, const void* s, size_t n, hipMemcpyKind
   std::memcpy(d, s, n);
   return hipSuccess;
 }
+inline hipError_t hipMemcpy(void* d, const void* s, size_t n, hipMemcpyKind) {
+  std::memcpy(d, s, n);
+  return hipSuccess;
+}
+inline hipError_t hipGetDevice(int* d) {
+  *d = 0;
+  return hipSuccess;
+}
+inline hipError_t hipSetDevice(int) { return hipSuccess; }
+inline hipError_t hipGetLastError() { return hipSuccess; }
 inline hipError_t hipDeviceSynchronize() { return hipSuccess; }
+inline hipError_t hipStreamIsCapturing(hipStream_t s, hipStreamCaptureStatus* c) {
+  *c = s && s->capturing ? hipStreamCaptureStatusActive : hipStreamCaptureStatusNone;
+  return hipSuccess;
+}
 inline hipError_t hipStreamCreateWithFlags(hipStream_t* s, unsigned) {
   *s = new MockHipStream{0};
   return hipSuccess;

@@ -209,6 +209,24 @@ int sq8_step_advance(int32_t* pos, int32_t* token, const int32_t* next, void*) {
   Line("sq8_step_advance").p(pos).p(token).p(next);
   return 0;
 }
+size_t sq8_packed_weight_bytes(int N, int K) {
+  return static_cast<size_t>((N + 15) / 16) * 16 * K;
+}
+// The packed layout computed on the host (byte 16 L + b of block (t, g) is w[16 t + L % 16]
+// [64 g + 16 (L / 16) + b], rows past N zero), so that callers' arguments can be checked.
+int sq8_pack_weights(const int8_t* w, int N, int K, int8_t* packed, void*) {
+  Line("sq8_pack_weights").p(w).i(N).i(K).p(packed);
+  const int T = (N + 15) / 16, G = K / 64;
+  for (int t = 0; t < T; ++t)
+    for (int g = 0; g < G; ++g)
+      for (int L = 0; L < 64; ++L)
+        for (int b = 0; b < 16; ++b) {
+          const int row = 16 * t + L % 16, col = 64 * g + 16 * (L / 16) + b;
+          packed[((static_cast<size_t>(t) * G + g) * 64 + L) * 16 + b] =
+              row < N ? w[static_cast<size_t>(row) * K + col] : 0;
+        }
+  return 0;
+}
 int sq8_argmax_rows(const float* logits, int rows, int n, int32_t* out, void*) {
   Line("sq8_argmax_rows").p(logits).i(rows).i(n).p(out);
   return 0;

@@ -424,3 +424,24 @@ def test_native_model_and_scheduler_match_oracle(dev, tmp_path, packed):
     for p in prompts:
         s2.add_request(p)
     assert [q.generated_tokens for q in s2.run(max_steps=5000)] == got
+
+
+@pytest.mark.gpu
+def test_native_batch_model_from_file_matches_oracle(dev, tmp_path):
+    """The all-C++ continuous-batching path: model file -> model::DeviceWeights ->
+    model::PagedBatchModel driven by scheduler::Scheduler; tokens equal the oracle's."""
+    nat = importlib.import_module("llm_steadyinfer_amd.native_scheduler")
+    path = mf.write_random(tmp_path / "m.bin", TINY, 64, seed=23, w_std=0.2)
+    rng = np.random.default_rng(23)
+    prompts = [rng.integers(0, TINY.vocab, n).tolist() for n in (9, 1, 30, 17)]
+    n_new, max_seq, bs = 10, 64, 8
+    ref = [do.DecodeModel(mf.ModelFile(path), max_seq=max_seq).generate(p, n_new)[0]
+           for p in prompts]
+    model = nat.NativePagedBatchModel.from_file(path, max_rows=4, max_seq_len=max_seq,
+                                                num_blocks=4 * (max_seq // bs), block_size=bs)
+    print("native batch model from file created", flush=True)
+    s = nat.NativeScheduler(model, max_batch=4, max_seq_len=max_seq, max_gen_len=n_new,
+                            block_size=bs)
+    for p in prompts:
+        assert s.add_request(p) >= 0
+    assert [q.generated_tokens for q in s.run(max_steps=5000)] == ref

@@ -111,3 +111,16 @@ def test_native_decoder_matches_python_decoder_and_oracle(dev, tmp_path, use_gra
     assert got == ref
     assert N.generate(prompt, 12, use_graph=use_graph) == got  # reset between runs
     assert D.generate(prompt, 12) == got
+
+
+@pytest.mark.gpu
+def test_native_decoder_from_file_matches_oracle(dev, tmp_path):
+    """The all-C++ path: the INT8 model file read by model::Int8ModelFile, uploaded fused by
+    model::DeviceWeights, decoded by model::Int8Decoder; greedy tokens equal the oracle's."""
+    nat = importlib.import_module("llm_steadyinfer_amd.native_scheduler")
+    path = mf.write_random(tmp_path / "m.bin", TINY_MHA, 64, seed=22, w_std=0.2)
+    prompt = np.random.default_rng(22).integers(0, TINY_MHA.vocab, 9).tolist()
+    ref = do.DecodeModel(mf.ModelFile(path), max_seq=64).generate(prompt, 16)[0]
+    N = nat.NativeInt8Decoder.from_file(path, max_seq=64)
+    print("native decoder from file created", flush=True)
+    assert N.generate(prompt, 16) == ref

@@ -542,3 +542,77 @@ def test_native_decoder_replays_one_graph_per_token(tmp_path):
     steps_eager = sum(1 for l in eager if l.startswith("sq8_argmax_advance"))
     steps_graph = sum(1 for l in graph if l.startswith("sq8_argmax_advance"))
     assert steps_eager == 5 and steps_graph == 1
+
+
+# ----------------------------------------------------------------------------- device weights
+def _pack_ref(q):
+    N, K = q.shape
+    T, G = (N + 15) // 16, K // 64
+    pad = np.zeros((T * 16, K), np.int8)
+    pad[:N] = q
+    return pad.reshape(T, 16, G, 4, 16).transpose(0, 2, 3, 1, 4).reshape(-1)
+
+
+@pytest.mark.parametrize("vocab,packed", [(-300, False), (-300, True), (300, False)])
+def test_device_weights_upload_layout(tmp_path, vocab, packed):
+    """model::DeviceWeights (C++) uploads a model file (read by the C++ loader) as the fused
+    weights the native models take: QKV = [wq; wk; wv], gate/up = [w1; w3] with scales
+    concatenated, optionally in the packed layout, plus the embedding and the norms; equal byte
+    for byte to the same layout built in numpy from the Python reader. vocab > 0 is the
+    reference's tied layout. Built with g++ against host stand-ins of HIP and libsq8."""
+    import shutil
+    import subprocess
+    from conftest import REPO
+    if shutil.which("g++") is None:
+        pytest.skip("g++ not available")
+    mf = importlib.import_module("llm_steadyinfer_amd.model_file")
+    cfg = mf.ModelConfig(dim=128, hidden_dim=192, layer_num=2, head_num=4, kv_head_num=2,
+                         vocab_size=vocab, seq_len=64, rope_theta=1e4)
+    path = mf.write_random(tmp_path / "m.bin", cfg, 64, seed=5, w_std=0.1)
+    exe = _EXE.get("weights") or tmp_path / "test_device_weights"
+    cpp, t = REPO / "llm-steadyinfer_amd" / "cpp", REPO / "tests" / "cpp"
+    srcs = [str(cpp / "src" / f"{f}.cpp") for f in ("alloc", "buffer", "tensor", "layer", "matmul",
+                                                    "int8_model_file", "hip_config",
+                                                    "device_weights")]
+    if not exe.exists():
+        res = subprocess.run(["g++", "-std=c++17", "-O1", "-g", "-fsanitize=address,undefined",
+                              "-fno-sanitize-recover=undefined", "-I", str(t / "mock_hip"), "-I",
+                              str(cpp / "include"), "-I", str(t),
+                              str(t / "test_device_weights.cpp"), str(t / "mock_sq8.cpp")] +
+                             srcs + ["-o", str(exe)], capture_output=True, text=True, timeout=300)
+        assert res.returncode == 0, res.stderr[-3000:]
+        _EXE["weights"] = exe
+    out = tmp_path / "uploaded.bin"
+    res = subprocess.run([str(exe), str(path), str(int(packed)), str(out)], capture_output=True,
+                         text=True, timeout=120)
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-3000:]
+    m = mf.ModelFile(path)
+    parts = []
+
+    def fused(names, layer):
+        qs, ss = zip(*(m.quant(n, layer) for n in names))
+        q = np.concatenate(qs, axis=0)
+        parts.append(_pack_ref(q) if packed else q.reshape(-1))
+        parts.append(np.concatenate(ss).astype(np.float32).view(np.int8))
+    for l in range(cfg.layer_num):
+        fused(("wq", "wk", "wv"), l)
+        fused(("wo",), l)
+        fused(("w1", "w3"), l)
+        fused(("w2",), l)
+    fused(("cls",), 0)
+    parts.append(np.asarray(m.fp32("embedding"), np.float32).reshape(-1).view(np.int8))
+    for i in range(2 * cfg.layer_num + 1):
+        parts.append(np.asarray(m.fp32("rmsnorm", i), np.float32).reshape(-1).view(np.int8))
+    want = np.concatenate(parts)
+    got = np.fromfile(out, np.int8)
+    assert got.size == want.size and np.array_equal(got, want)
+    assert res.stdout.splitlines()[0] == f"config 128 192 2 4 2 300 64"
+    assert res.stdout.count("sq8_pack_weights") == (4 * cfg.layer_num + 1 if packed else 0)
+
+
+def test_native_from_file_reports_a_missing_file(tmp_path):
+    """The C++ file path fails cleanly (no device work) for a file that does not exist."""
+    with pytest.raises(RuntimeError, match="native decoder"):
+        native.NativeInt8Decoder.from_file(tmp_path / "missing.bin", max_seq=64)
+    with pytest.raises(RuntimeError, match="native batch model"):
+        native.NativePagedBatchModel.from_file(tmp_path / "missing.bin", 4, 64, 16, 4)
