@@ -91,36 +91,3 @@ def test_qwen2_1_5b_shapes_random_init(dev):
     c = D.generate(prompt, 8, use_graph=False)
     assert a == b == c
     assert all(0 <= t < mf.QWEN2_1_5B.vocab for t in a)
-
-
-@pytest.mark.gpu
-@pytest.mark.parametrize("use_graph", [True, False])
-def test_native_decoder_matches_python_decoder_and_oracle(dev, tmp_path, use_graph):
-    """model::Int8Decoder (C++ host loop, one graph replay per token) on the weights of the
-    Python decoder: greedy tokens equal the Python decoder's and the float64 oracle's."""
-    nat = importlib.import_module("llm_steadyinfer_amd.native_scheduler")
-    cfg = mf.ModelConfig(dim=256, hidden_dim=512, layer_num=2, head_num=4, kv_head_num=2,
-                         vocab_size=-1000, seq_len=96, rope_theta=1e6)
-    path = mf.write_random(tmp_path / "m.bin", cfg, 64, seed=21, w_std=0.2)
-    prompt = np.random.default_rng(21).integers(0, cfg.vocab, 17).tolist()
-    D = _decoder_mod().Int8Decoder.from_file(path, max_seq=96, device=dev)
-    ref = do.DecodeModel(mf.ModelFile(path), max_seq=96).generate(prompt, 12)[0]
-    N = nat.NativeInt8Decoder(D.cfg, D.w, D.gs, max_seq=96)
-    print("native decoder created", flush=True)
-    got = N.generate(prompt, 12, use_graph=use_graph)
-    assert got == ref
-    assert N.generate(prompt, 12, use_graph=use_graph) == got  # reset between runs
-    assert D.generate(prompt, 12) == got
-
-
-@pytest.mark.gpu
-def test_native_decoder_from_file_matches_oracle(dev, tmp_path):
-    """The all-C++ path: the INT8 model file read by model::Int8ModelFile, uploaded fused by
-    model::DeviceWeights, decoded by model::Int8Decoder; greedy tokens equal the oracle's."""
-    nat = importlib.import_module("llm_steadyinfer_amd.native_scheduler")
-    path = mf.write_random(tmp_path / "m.bin", TINY_MHA, 64, seed=22, w_std=0.2)
-    prompt = np.random.default_rng(22).integers(0, TINY_MHA.vocab, 9).tolist()
-    ref = do.DecodeModel(mf.ModelFile(path), max_seq=64).generate(prompt, 16)[0]
-    N = nat.NativeInt8Decoder.from_file(path, max_seq=64)
-    print("native decoder from file created", flush=True)
-    assert N.generate(prompt, 16) == ref
