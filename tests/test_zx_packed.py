@@ -1,4 +1,5 @@
-"""GPU tests of the packed weight layout (sq8_pack_weights and the _packed entry points).
+"""GPU tests of the packed weight layout (sq8_pack_weights and the _packed entry points),
+collected after the row-major parity tests.
 
 - The packed bytes equal a numpy restatement of the documented layout (16-row tiles, each 64-wide
   group of a tile one 1 KiB block in lane order, padding rows zero).
@@ -219,3 +220,14 @@ def test_packed_graph_replays_match_eager(sq8, dev):
             torch.cuda.synchronize()
             assert torch.equal(y, eager), M
         outs[M] = eager
+
+
+@pytest.mark.parametrize("max_batch,block_size,num_blocks", [(4, 4, 24), (96, 8, None)])
+def test_packed_continuous_batching_matches_oracle(sq8, dev, tmp_path, max_batch, block_size,
+                                                   num_blocks):
+    """tests/test_batch.py's continuous-batching oracle test with the model on packed weights
+    (every matmul through the _packed entry points): with preemption at 4 rows, and through the
+    fused-epilogue GEMM at 96 rows."""
+    import test_batch
+    test_batch.test_continuous_batching_matches_oracle(sq8, dev, tmp_path, max_batch, block_size,
+                                                       num_blocks, True, True)
