@@ -348,13 +348,34 @@ def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed:
     wall = time.perf_counter() - t0
     done = [q for q in s.finished if q.id not in warm]
     gen_tokens = sum(len(q.generated_tokens) for q in done)
+    # Per-request latencies as the reference's offline benchmark computes them
+    # (benchmark/offline_batch_benchmark.cpp:280-324): TTFT = first token - admission, E2E =
+    # finish - admission, TPOT = (E2E - TTFT) / (tokens - 1), ITL = the gaps between tokens;
+    # nearest-rank percentiles (bench_common.h:95-101).
+    def pct(v, p):
+        if not v:
+            return 0.0
+        v = sorted(v)
+        return v[min(len(v) - 1, max(0, int(np.ceil(p / 100.0 * len(v))) - 1))]
+    ttft = [(q.first_token_time - q.admit_time) * 1e3 for q in done if q.generated_tokens]
+    e2e = [(q.finish_time - q.admit_time) * 1e3 for q in done if q.generated_tokens]
+    tpot = [(e - t) / (len(q.generated_tokens) - 1) for q, t, e in
+            zip([q for q in done if q.generated_tokens], ttft, e2e)
+            if len(q.generated_tokens) > 1]
+    itl = [g for q in done for g in q.token_timestamps_ms]
+    mean = lambda v: float(np.mean(v)) if v else 0.0
+    latency = {"ttft_avg_ms": round(mean(ttft), 2), "ttft_p50_ms": round(pct(ttft, 50), 2),
+               "ttft_p99_ms": round(pct(ttft, 99), 2), "tpot_avg_ms": round(mean(tpot), 3),
+               "tpot_p50_ms": round(pct(tpot, 50), 3), "tpot_p99_ms": round(pct(tpot, 99), 3),
+               "itl_avg_ms": round(mean(itl), 3), "itl_p99_ms": round(pct(itl, 99), 3),
+               "e2e_avg_ms": round(mean(e2e), 1), "e2e_p99_ms": round(pct(e2e, 99), 1)}
     prompt_tokens = int(lens.sum())
     return {"workload": f"config 5: Llama-3-8B-shaped random-init INT8 model, {n_seqs} sequences, "
                         f"lognormal prompts (median 200, sigma {sigma}, clipped 16..2048; "
                         f"mean {lens.mean():.0f}, max {int(lens.max())}), {n_new} greedy tokens "
                         f"each, paged KV block {block}, max_batch 64" +
                         (", packed weights" if packed else ""),
-            "output_tokens_per_s": round(gen_tokens / wall, 1),
+            "output_tokens_per_s": round(gen_tokens / wall, 1), "latency": latency,
             "total_tokens_per_s": round((gen_tokens + prompt_tokens) / wall, 1),
             "wall_s": round(wall, 3), "generated_tokens": gen_tokens,
             "prompt_tokens": prompt_tokens, "steps": s.steps - steps0,

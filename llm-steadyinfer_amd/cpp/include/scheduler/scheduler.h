@@ -30,7 +30,9 @@
 //    sequence queued);
 //  - a victim cut back into its prompt resumes its prefill at min(its progress, the cut) (the
 //    reference resumes at the cut, skipping positions never written).
-// Timing statistics are not carried over.
+// Serving timestamps are kept per Sequence as the reference keeps them, and
+// get_batch_reconstruct_times_ms() holds, per decode-only step, the host time spent forming the
+// rows and block tables.
 #ifndef SQ8_OP_SCHEDULER_SCHEDULER_H_
 #define SQ8_OP_SCHEDULER_SCHEDULER_H_
 #include <cstdint>
@@ -95,6 +97,12 @@ class Scheduler {
   const std::vector<Sequence>& get_finished() const { return finished_sequences_; }
   std::vector<const Sequence*> get_running() const;
   int num_waiting() const { return static_cast<int>(waiting_queue_.size()); }
+  const std::vector<double>& get_batch_reconstruct_times_ms() const {
+    return batch_reconstruct_times_ms_;
+  }
+  // The running or finished sequence with this id (nullptr if none).
+  const Sequence* find_sequence(int id) const;
+  TimePoint created() const { return created_; }
   int get_block_size() const { return block_size_; }
   int get_max_kv_seq_len() const { return max_seq_len_; }
   int get_busy_kv_slots() const { return static_cast<int>(running_.size()); }
@@ -134,7 +142,7 @@ class Scheduler {
   void truncate_sequence(Sequence& seq, int keep_blocks);
   bool ensure_blocks_for(Sequence* seq, int position, const std::vector<int>& protect);
   std::vector<BatchRow> build_batch_rows();
-  base::Status execute_batch(const std::vector<BatchRow>& rows);
+  base::Status execute_batch(const std::vector<BatchRow>& rows, TimePoint t0);
   void update_sequences();
   void retire(Sequence* seq);
 
@@ -146,6 +154,8 @@ class Scheduler {
   std::vector<Sequence*> running_;
   std::vector<Sequence> finished_sequences_;
   std::vector<StepRow> last_rows_;
+  std::vector<double> batch_reconstruct_times_ms_;
+  TimePoint created_ = std::chrono::steady_clock::now();
   int max_batch_size_;
   int max_seq_len_;
   int max_gen_len_;

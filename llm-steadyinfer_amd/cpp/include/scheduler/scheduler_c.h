@@ -51,6 +51,13 @@ int sq8_sched_finished_ids(void* sched, int32_t* out, int cap);
 /* The last step's rows as (seq id, is_decode, token, position) quadruples (up to cap rows); the
  * row count. */
 int sq8_sched_last_rows(void* sched, int32_t* out, int cap);
+/* Serving timestamps of a running or finished sequence, in ms since the scheduler was created
+ * (-1 when not reached yet): times[0..4] = arrival, admission, first token, last token, finish;
+ * its inter-token gaps in ms go to itl (up to cap). Returns the number of gaps, or
+ * SQ8_SCHED_ERR_UNKNOWN. */
+int sq8_sched_timing(void* sched, int seq_id, double* times, double* itl, int cap);
+/* Host ms spent forming each decode-only step's rows (up to cap); returns the count. */
+int sq8_sched_batch_reconstruct_times(void* sched, double* out, int cap);
 /* Reference count of a physical block (0 when free or out of range). */
 int sq8_sched_block_ref(void* sched, int block);
 /* 1 when the block pool's invariant holds. */

@@ -45,6 +45,7 @@ int Scheduler::add_request(const std::vector<int>& prompt_tokens) {
   seq->prompt_tokens = prompt_tokens;
   seq->num_prompt_tokens = n;
   seq->max_gen_len = std::max(1, std::min(max_gen_len_, max_seq_len_ - n));
+  seq->arrival_time = std::chrono::steady_clock::now();
   Sequence* p = seq.get();
   store_.emplace(p->id, std::move(seq));
   waiting_queue_.push_back(p);
@@ -76,6 +77,7 @@ void Scheduler::try_admit_sequences() {
     if (seq->state == SeqState::PREEMPTED) {
       waiting_queue_.pop_front();
       seq->state = SeqState::RUNNING;
+      seq->admit_time = std::chrono::steady_clock::now();
       running_.push_back(seq);
       continue;
     }
@@ -100,8 +102,19 @@ void Scheduler::try_admit_sequences() {
     seq->kv_slot_id = row;
     seq->num_blocks_allocated = need;
     seq->state = SeqState::RUNNING;
+    seq->admit_time = std::chrono::steady_clock::now();
     running_.push_back(seq);
   }
+}
+
+const Sequence* Scheduler::find_sequence(int id) const {
+  for (const Sequence* s : running_)
+    if (s->id == id) return s;
+  const auto it = store_.find(id);
+  if (it != store_.end()) return it->second.get();
+  for (const Sequence& s : finished_sequences_)
+    if (s.id == id) return &s;
+  return nullptr;
 }
 
 bool Scheduler::try_preempt_for(int need_blocks, int skip_seq_id,
@@ -233,7 +246,7 @@ std::vector<Scheduler::BatchRow> Scheduler::build_batch_rows() {
 }
 
 // ---------------------------------------------------------------- one step
-base::Status Scheduler::execute_batch(const std::vector<BatchRow>& rows) {
+base::Status Scheduler::execute_batch(const std::vector<BatchRow>& rows, TimePoint t0) {
   const int batch = static_cast<int>(rows.size());
   int nd = 0;
   for (const BatchRow& r : rows) nd += r.is_decode;
@@ -249,12 +262,24 @@ base::Status Scheduler::execute_batch(const std::vector<BatchRow>& rows) {
     alloc_->copy_block_table_row(rows[i].seq->kv_slot_id,
                                  &table_[static_cast<size_t>(i) * max_blocks_per_seq_]);
   }
+  if (nd == batch)
+    batch_reconstruct_times_ms_.push_back(
+        std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0)
+            .count());
   base::Status st = model_->forward_batch(batch, nd, tokens_.data(), positions_.data(),
                                           seq_ids_.data(), table_.data(), max_blocks_per_seq_,
                                           next_.data());
   if (!st) return st;
+  const TimePoint now = std::chrono::steady_clock::now();
   for (int i = 0; i < nd; ++i) {
     Sequence* s = rows[i].seq;
+    if (s->generated_tokens.empty()) {
+      s->first_token_time = now;
+    } else {
+      s->token_timestamps_ms.push_back(
+          std::chrono::duration<double, std::milli>(now - s->last_token_time).count());
+    }
+    s->last_token_time = now;
     s->generated_tokens.push_back(next_[i]);
     s->num_generated_tokens = static_cast<int>(s->generated_tokens.size());
   }
@@ -264,12 +289,13 @@ base::Status Scheduler::execute_batch(const std::vector<BatchRow>& rows) {
 
 base::Status Scheduler::step() {
   try_admit_sequences();
+  const TimePoint t0 = std::chrono::steady_clock::now();
   const std::vector<BatchRow> rows = build_batch_rows();
   last_rows_.clear();
   for (const BatchRow& r : rows)
     last_rows_.push_back(StepRow{r.seq->id, r.is_decode, r.token_id, r.position});
   base::Status st = base::error::Success();
-  if (!rows.empty()) st = execute_batch(rows);
+  if (!rows.empty()) st = execute_batch(rows, t0);
   ++steps_;
   if (!st) {  // unrecoverable forward failure: retire every running sequence
     for (Sequence* s : running_) s->is_finished = true;
@@ -281,6 +307,7 @@ base::Status Scheduler::step() {
 void Scheduler::retire(Sequence* s) {
   s->is_finished = true;
   s->state = SeqState::FINISHED;
+  s->finish_time = std::chrono::steady_clock::now();
   alloc_->free_all(s->kv_slot_id);
   finished_sequences_.push_back(*s);
   store_.erase(s->id);

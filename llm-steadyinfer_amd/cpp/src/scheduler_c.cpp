@@ -146,6 +146,34 @@ int sq8_sched_last_rows(void* sched, int32_t* out, int cap) {
   return n;
 }
 
+int sq8_sched_timing(void* sched, int seq_id, double* times, double* itl, int cap) {
+  if (!sched || !times || cap < 0 || (cap > 0 && !itl)) return SQ8_SCHED_ERR_ARG;
+  const scheduler::Scheduler& s = *get(sched)->sched;
+  const scheduler::Sequence* q = s.find_sequence(seq_id);
+  if (!q) return SQ8_SCHED_ERR_UNKNOWN;
+  const scheduler::TimePoint t0 = s.created();
+  auto ms = [&](scheduler::TimePoint t) {
+    return t == scheduler::TimePoint{} ? -1.0
+                                       : std::chrono::duration<double, std::milli>(t - t0).count();
+  };
+  times[0] = ms(q->arrival_time);
+  times[1] = ms(q->admit_time);
+  times[2] = ms(q->first_token_time);
+  times[3] = ms(q->last_token_time);
+  times[4] = ms(q->finish_time);
+  const int n = static_cast<int>(q->token_timestamps_ms.size());
+  std::copy_n(q->token_timestamps_ms.begin(), std::min(n, cap), itl);
+  return n;
+}
+
+int sq8_sched_batch_reconstruct_times(void* sched, double* out, int cap) {
+  if (!sched || cap < 0 || (cap > 0 && !out)) return SQ8_SCHED_ERR_ARG;
+  const auto& v = get(sched)->sched->get_batch_reconstruct_times_ms();
+  const int n = static_cast<int>(v.size());
+  std::copy_n(v.begin(), std::min(n, cap), out);
+  return n;
+}
+
 int sq8_sched_block_ref(void* sched, int block) {
   if (!sched) return SQ8_SCHED_ERR_ARG;
   return get(sched)->sched->block_allocator().ref_count(block);

@@ -23,7 +23,7 @@ SCHED_SYMBOLS = ("sq8_sched_create", "sq8_sched_destroy", "sq8_sched_set_stop_to
                  "sq8_sched_add_request", "sq8_sched_step", "sq8_sched_run",
                  "sq8_sched_all_finished", "sq8_sched_stats", "sq8_sched_generated",
                  "sq8_sched_finished_ids", "sq8_sched_last_rows", "sq8_sched_block_ref",
-                 "sq8_sched_invariant")
+                 "sq8_sched_invariant", "sq8_sched_timing", "sq8_sched_batch_reconstruct_times")
 SQ8_SCHED_OK, SQ8_SCHED_ERR_ARG, SQ8_SCHED_ERR_MODEL, SQ8_SCHED_ERR_STEPS = 0, -1, -2, -3
 
 _P32 = ctypes.POINTER(ctypes.c_int32)
@@ -55,6 +55,9 @@ def op_lib() -> ctypes.CDLL:
         L.sq8_sched_last_rows.argtypes = [vp, _P32, I]
         L.sq8_sched_block_ref.argtypes = [vp, I]
         L.sq8_sched_invariant.argtypes = [vp]
+        PD = ctypes.POINTER(ctypes.c_double)
+        L.sq8_sched_timing.argtypes = [vp, I, PD, PD, I]
+        L.sq8_sched_batch_reconstruct_times.argtypes = [vp, PD, I]
         for name in SCHED_SYMBOLS:
             if name not in ("sq8_sched_create", "sq8_sched_destroy"):
                 getattr(L, name).restype = I
@@ -83,9 +86,17 @@ class Row:
 
 @dataclass
 class FinishedSequence:
+    """A finished request; times in seconds on the scheduler's clock (its creation is 0), as
+    scheduler.Sequence's are on time.perf_counter()."""
     id: int
     prompt_tokens: List[int]
     generated_tokens: List[int] = field(default_factory=list)
+    arrival_time: float = 0.0
+    admit_time: float = 0.0
+    first_token_time: float = 0.0
+    last_token_time: float = 0.0
+    finish_time: float = 0.0
+    token_timestamps_ms: List[float] = field(default_factory=list)
 
 
 class NativeScheduler:
@@ -233,7 +244,24 @@ class NativeScheduler:
         n = self._check(L.sq8_sched_finished_ids(self._h, None, 0))
         buf = (ctypes.c_int32 * max(n, 1))()
         L.sq8_sched_finished_ids(self._h, buf, n)
-        return [FinishedSequence(i, self._prompts[i], self.generated(i)) for i in buf[:n]]
+        return [self._finished(i) for i in buf[:n]]
+
+    def _finished(self, i: int) -> FinishedSequence:
+        L = op_lib()
+        times = (ctypes.c_double * 5)()
+        n = self._check(L.sq8_sched_timing(self._h, i, times, None, 0))
+        itl = (ctypes.c_double * max(n, 1))()
+        L.sq8_sched_timing(self._h, i, times, itl, n)
+        t = [v / 1e3 for v in times]
+        return FinishedSequence(i, self._prompts[i], self.generated(i), *t, list(itl[:n]))
+
+    @property
+    def batch_reconstruct_times_ms(self) -> List[float]:
+        L = op_lib()
+        n = self._check(L.sq8_sched_batch_reconstruct_times(self._h, None, 0))
+        buf = (ctypes.c_double * max(n, 1))()
+        L.sq8_sched_batch_reconstruct_times(self._h, buf, n)
+        return list(buf[:n])
 
     def last_rows(self):
         """(seq id, is_decode, token, position) of each row of the last step."""

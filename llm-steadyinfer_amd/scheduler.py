@@ -56,11 +56,19 @@ Deliberate deviations in the prefix cache:
     block to a new sequence in the same row at the same index, and that block, holding the new
     sequence's KV, would pass both checks.
 Sentence-end tokens (update_sequences, :681-690): a sequence whose last generated token is one of
-`stop_tokens` retires (the reference asks the model's tokenizer, is_sentence_ending). Timing
-statistics are not carried over.
+`stop_tokens` retires (the reference asks the model's tokenizer, is_sentence_ending).
+
+Serving timestamps as the reference records them (sequence.h; scheduler.cpp:94, 187, 236, 263,
+507, 600-607, 641-647, 662-684), in seconds of time.perf_counter(): arrival_time at add_request,
+admit_time at each admission (a resumed sequence is re-stamped), first_token_time when a token
+lands on a sequence with none (again after a truncation that dropped them), last_token_time and
+the inter-token gaps token_timestamps_ms, finish_time at retirement. batch_reconstruct_times_ms
+holds, per decode-only step, the host time spent forming the rows and block tables (the
+reference times its pure-decode tensor setup, scheduler.cpp:560-572).
 """
 from __future__ import annotations
 
+import time
 from dataclasses import dataclass, field
 from typing import Callable, Dict, Iterable, List, Optional, Tuple
 
@@ -217,6 +225,12 @@ class Sequence:
     prefill_complete: bool = False
     finished: bool = False
     shared_blocks: int = 0  # prompt blocks mounted from the prefix cache at admission
+    arrival_time: float = 0.0
+    admit_time: float = 0.0
+    first_token_time: float = 0.0
+    last_token_time: float = 0.0
+    finish_time: float = 0.0
+    token_timestamps_ms: List[float] = field(default_factory=list)  # inter-token gaps
 
     @property
     def num_prompt(self) -> int:
@@ -258,6 +272,7 @@ class Scheduler:
         self.prefix = PrefixCache(block_size) if prefix_cache else None
         self.stop_tokens = frozenset(int(t) for t in stop_tokens)
         self.shared_prefix_blocks = 0  # blocks mounted from the prefix cache, over the run
+        self.batch_reconstruct_times_ms: List[float] = []  # per decode-only step
 
     @staticmethod
     def resolve_block_size(avg_prompt_len: float) -> int:
@@ -274,6 +289,7 @@ class Scheduler:
             return -1
         seq = Sequence(self.next_id, list(prompt),
                        max(1, min(self.max_gen_len, self.max_seq_len - len(prompt))))
+        seq.arrival_time = time.perf_counter()
         self.next_id += 1
         self.waiting.append(seq)
         return seq.id
@@ -288,6 +304,7 @@ class Scheduler:
             if seq.state == PREEMPTED:
                 self.waiting.pop(0)
                 seq.state = RUNNING
+                seq.admit_time = time.perf_counter()
                 self.running.append(seq)
                 continue
             need = (seq.num_prompt + self.block_size - 1) // self.block_size
@@ -307,6 +324,7 @@ class Scheduler:
                 seq.shared_blocks = len(shared)
                 self.shared_prefix_blocks += len(shared)
             seq.kv_row, seq.num_blocks, seq.state = row, need, RUNNING
+            seq.admit_time = time.perf_counter()
             self.running.append(seq)
 
     def _lookup(self, seq: Sequence) -> List[int]:
@@ -426,14 +444,24 @@ class Scheduler:
     # ------------------------------------------------------------------ one step
     def step(self) -> None:
         self._admit()
+        t0 = time.perf_counter()
         rows = self.build_rows()
         if rows:
             tables = [self.alloc.table_row(r.seq.kv_row) for r in rows]
-            tokens = self.forward(rows, tables)
             nd = sum(1 for r in rows if r.is_decode)
+            if nd == len(rows):
+                self.batch_reconstruct_times_ms.append((time.perf_counter() - t0) * 1e3)
+            tokens = self.forward(rows, tables)
             assert len(tokens) == nd
+            now = time.perf_counter()
             for r, t in zip(rows[:nd], tokens):
-                r.seq.generated_tokens.append(int(t))
+                q = r.seq
+                if not q.generated_tokens:
+                    q.first_token_time = now
+                else:
+                    q.token_timestamps_ms.append((now - q.last_token_time) * 1e3)
+                q.last_token_time = now
+                q.generated_tokens.append(int(t))
             self.rows_run += len(rows)
         self.steps += 1
         self._retire()
@@ -445,6 +473,7 @@ class Scheduler:
                     s.generated_tokens[-1] in self.stop_tokens)
             if s.finished or stop or len(s.generated_tokens) >= s.max_gen_len:
                 s.finished, s.state = True, FINISHED
+                s.finish_time = time.perf_counter()
                 self.alloc.free_all(s.kv_row)
                 self.finished.append(s)
             else:

@@ -616,3 +616,30 @@ def test_native_from_file_reports_a_missing_file(tmp_path):
         native.NativeInt8Decoder.from_file(tmp_path / "missing.bin", max_seq=64)
     with pytest.raises(RuntimeError, match="native batch model"):
         native.NativePagedBatchModel.from_file(tmp_path / "missing.bin", 4, 64, 16, 4)
+
+
+@pytest.mark.parametrize("kind", ["python", "native"])
+def test_serving_timestamps(kind):
+    """Per-request timestamps as the reference records them: arrival <= admission <= first
+    token <= last token <= finish; one inter-token gap per generated token after the first, the
+    gaps summing to last - first; one batch-reconstruct time per decode-only step."""
+    import time as _t
+    calls = []
+
+    def model(rows, tables):
+        _t.sleep(0.0005)
+        calls.append(all(r.is_decode for r in rows))
+        return [1] * sum(r.is_decode for r in rows)
+    cls = Scheduler if kind == "python" else NativeScheduler
+    s = cls(model, max_batch=3, max_seq_len=64, max_gen_len=6, block_size=4)
+    for n in (5, 9, 2, 17):
+        s.add_request(list(range(1, n + 1)))
+    done = s.run(max_steps=1000)
+    for q in done:
+        assert q.arrival_time <= q.admit_time <= q.first_token_time <= q.last_token_time \
+            <= q.finish_time, q.id
+        assert len(q.token_timestamps_ms) == len(q.generated_tokens) - 1
+        assert abs(sum(q.token_timestamps_ms) / 1e3 - (q.last_token_time - q.first_token_time)) \
+            < 1e-6
+        assert min(q.token_timestamps_ms) > 0.4  # each step sleeps 0.5 ms
+    assert len(s.batch_reconstruct_times_ms) == sum(calls) > 0
