@@ -27,6 +27,7 @@ int main() {
   int packed = 0, graphs = 0, split = 0;
   if (!(std::cin >> mode)) return 2;
   if (mode == "batch" && !(std::cin >> packed >> graphs >> split)) return 2;
+  // mode "validate": forward_batch refuses bad rows before any launch.
   model::BatchModelConfig c;
   c.dim = 64;
   c.hidden_dim = 96;
@@ -66,6 +67,34 @@ int main() {
     mock_print_log();
     for (void* p : bufs) std::free(p);
     return 0;
+  }
+  if (mode == "validate") {  // host-side refusals: nothing may reach libsq8
+    model::PagedBatchModel m(c, w, 8, 64, 40, 4, nullptr, true, true);
+    if (!m.init()) return 1;
+    const int S = m.max_blocks_per_seq();
+    std::vector<int32_t> tab(8 * S, -1), next(8);
+    tab[0] = 3;  // row 0 holds block 3 at index 0 only
+    int32_t tok[8] = {1, 2, 3, 4, 5, 6, 7, 8}, pos[8] = {0};
+    struct Case {
+      const char* what;
+      int B, nd, stride, pos0, tok0;
+    } cases[] = {{"no rows", 0, 0, S, 0, 1},          {"too many rows", 9, 0, S, 0, 1},
+                 {"decode rows > rows", 1, 2, S, 0, 1}, {"table width", 1, 1, S - 1, 0, 1},
+                 {"position past max_seq", 1, 1, S, 64, 1},
+                 {"unmapped block", 1, 1, S, 4, 1},     {"token id", 1, 1, S, 0, 50},
+                 {"negative token", 1, 1, S, 0, -1}};
+    int failures = 0;
+    for (const Case& k : cases) {
+      pos[0] = k.pos0;
+      tok[0] = k.tok0;
+      const base::Status st = m.forward_batch(k.B, k.nd, tok, pos, nullptr, tab.data(),
+                                              k.stride, next.data());
+      std::printf("%s: %s\n", k.what, st ? "accepted" : st.get_err_msg().c_str());
+      failures += static_cast<bool>(st);
+    }
+    mock_print_log();  // only the rope tables of init()
+    for (void* p : bufs) std::free(p);
+    return failures;
   }
   model::PagedBatchModel m(c, w, 8, 64, 40, 4, nullptr, graphs != 0, split != 0);
   base::Status st = m.init();

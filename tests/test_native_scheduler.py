@@ -643,3 +643,18 @@ def test_serving_timestamps(kind):
             < 1e-6
         assert min(q.token_timestamps_ms) > 0.4  # each step sleeps 0.5 ms
     assert len(s.batch_reconstruct_times_ms) == sum(calls) > 0
+
+
+def test_native_model_refuses_bad_rows_before_launching(tmp_path):
+    """model::PagedBatchModel::forward_batch checks every row on the host (row counts, table
+    width, position range, a cache block mapped for every position attended, token ids) and
+    refuses with nothing launched: a bad table would otherwise become an out-of-bounds read."""
+    import subprocess
+    exe = _calls_exe(tmp_path)
+    res = subprocess.run([str(exe)], input="validate\n", capture_output=True, text=True,
+                         timeout=60)
+    assert res.returncode == 0, res.stdout + res.stderr[-2000:]
+    lines = res.stdout.splitlines()
+    assert sum(1 for l in lines if ": " in l and "accepted" not in l) == 8
+    calls = [l for l in lines if l.startswith("sq8_")]
+    assert len(calls) == 1 and calls[0].startswith("sq8_rope_tables")  # init() only
