@@ -342,8 +342,19 @@ def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed:
     for p in prompts:
         s.add_request(p)
     torch.cuda.synchronize()
+    # Step loop with the KV occupancy sampled before every step, as the reference's offline
+    # benchmark does (benchmark/offline_batch_benchmark.cpp:240-268; host-side reads only).
+    used_sum = alloc_sum = busy_sum = samples = peak_busy = 0
     t0 = time.perf_counter()
-    s.run()
+    while not s.all_finished():
+        busy, used, alloc = s.kv_snapshot()
+        if busy > 0:
+            used_sum += used
+            alloc_sum += alloc
+            busy_sum += busy
+            peak_busy = max(peak_busy, busy)
+            samples += 1
+        s.step()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     done = [q for q in s.finished if q.id not in warm]
@@ -369,6 +380,13 @@ def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed:
                "tpot_p50_ms": round(pct(tpot, 50), 3), "tpot_p99_ms": round(pct(tpot, 99), 3),
                "itl_avg_ms": round(mean(itl), 3), "itl_p99_ms": round(pct(itl, 99), 3),
                "e2e_avg_ms": round(mean(e2e), 1), "e2e_p99_ms": round(pct(e2e, 99), 1)}
+    util = used_sum / alloc_sum if alloc_sum else 0.0
+    kv = {"kv_cache_util_global": round(util, 4), "kv_cache_frag_global": round(1 - util, 4),
+          "kv_cache_frag_per_seq": round(mean([1 - (len(q.prompt_tokens) +
+                                                    len(q.generated_tokens)) / max_seq
+                                               for q in done]), 4),
+          "avg_busy_kv_slots": round(busy_sum / samples, 2) if samples else 0.0,
+          "peak_busy_kv_slots": peak_busy}
     prompt_tokens = int(lens.sum())
     return {"workload": f"config 5: Llama-3-8B-shaped random-init INT8 model, {n_seqs} sequences, "
                         f"lognormal prompts (median 200, sigma {sigma}, clipped 16..2048; "
@@ -376,6 +394,7 @@ def batch_run(torch, weights, lm_head, n_seqs: int = 64, n_new: int = 128, seed:
                         f"each, paged KV block {block}, max_batch 64" +
                         (", packed weights" if packed else ""),
             "output_tokens_per_s": round(gen_tokens / wall, 1), "latency": latency,
+            "kv_cache": kv,
             "total_tokens_per_s": round((gen_tokens + prompt_tokens) / wall, 1),
             "wall_s": round(wall, 3), "generated_tokens": gen_tokens,
             "prompt_tokens": prompt_tokens, "steps": s.steps - steps0,

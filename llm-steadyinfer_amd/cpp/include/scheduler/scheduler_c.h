@@ -58,6 +58,10 @@ int sq8_sched_last_rows(void* sched, int32_t* out, int cap);
 int sq8_sched_timing(void* sched, int seq_id, double* times, double* itl, int cap);
 /* Host ms spent forming each decode-only step's rows (up to cap); returns the count. */
 int sq8_sched_batch_reconstruct_times(void* sched, double* out, int cap);
+/* KV occupancy now (as the reference's offline benchmark samples it before every step): busy
+ * rows, tokens held by the running sequences, tokens of KV allocated to them. Returns the count
+ * written (at most n, 3 in all). */
+int sq8_sched_kv_snapshot(void* sched, int64_t* out, int n);
 /* Reference count of a physical block (0 when free or out of range). */
 int sq8_sched_block_ref(void* sched, int block);
 /* 1 when the block pool's invariant holds. */

@@ -174,6 +174,18 @@ int sq8_sched_batch_reconstruct_times(void* sched, double* out, int cap) {
   return n;
 }
 
+int sq8_sched_kv_snapshot(void* sched, int64_t* out, int n) {
+  if (!sched || n < 0 || (n > 0 && !out)) return SQ8_SCHED_ERR_ARG;
+  const scheduler::Scheduler& s = *get(sched)->sched;
+  int64_t used = 0;
+  for (const scheduler::Sequence* q : s.get_running())
+    used += q->num_prompt_tokens + static_cast<int64_t>(q->generated_tokens.size());
+  const int64_t v[] = {s.get_busy_kv_slots(), used, s.get_allocated_kv_tokens()};
+  const int count = std::min(n, 3);
+  std::copy(v, v + count, out);
+  return count;
+}
+
 int sq8_sched_block_ref(void* sched, int block) {
   if (!sched) return SQ8_SCHED_ERR_ARG;
   return get(sched)->sched->block_allocator().ref_count(block);

@@ -23,7 +23,8 @@ SCHED_SYMBOLS = ("sq8_sched_create", "sq8_sched_destroy", "sq8_sched_set_stop_to
                  "sq8_sched_add_request", "sq8_sched_step", "sq8_sched_run",
                  "sq8_sched_all_finished", "sq8_sched_stats", "sq8_sched_generated",
                  "sq8_sched_finished_ids", "sq8_sched_last_rows", "sq8_sched_block_ref",
-                 "sq8_sched_invariant", "sq8_sched_timing", "sq8_sched_batch_reconstruct_times")
+                 "sq8_sched_invariant", "sq8_sched_timing", "sq8_sched_batch_reconstruct_times",
+                 "sq8_sched_kv_snapshot")
 SQ8_SCHED_OK, SQ8_SCHED_ERR_ARG, SQ8_SCHED_ERR_MODEL, SQ8_SCHED_ERR_STEPS = 0, -1, -2, -3
 
 _P32 = ctypes.POINTER(ctypes.c_int32)
@@ -58,6 +59,7 @@ def op_lib() -> ctypes.CDLL:
         PD = ctypes.POINTER(ctypes.c_double)
         L.sq8_sched_timing.argtypes = [vp, I, PD, PD, I]
         L.sq8_sched_batch_reconstruct_times.argtypes = [vp, PD, I]
+        L.sq8_sched_kv_snapshot.argtypes = [vp, ctypes.POINTER(ctypes.c_int64), I]
         for name in SCHED_SYMBOLS:
             if name not in ("sq8_sched_create", "sq8_sched_destroy"):
                 getattr(L, name).restype = I
@@ -270,6 +272,12 @@ class NativeScheduler:
         buf = (ctypes.c_int32 * max(4 * n, 1))()
         L.sq8_sched_last_rows(self._h, buf, n)
         return [tuple(buf[4 * i:4 * i + 4]) for i in range(n)]
+
+    def kv_snapshot(self):
+        """(busy KV rows, tokens held by the running sequences, tokens of KV allocated)."""
+        out = (ctypes.c_int64 * 3)()
+        self._check(op_lib().sq8_sched_kv_snapshot(self._h, out, 3))
+        return tuple(out)
 
     def block_ref(self, block: int) -> int:
         return self._check(op_lib().sq8_sched_block_ref(self._h, block))

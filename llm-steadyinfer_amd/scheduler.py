@@ -297,6 +297,15 @@ class Scheduler:
     def all_finished(self) -> bool:
         return not self.waiting and not self.running
 
+    def kv_snapshot(self) -> Tuple[int, int, int]:
+        """(busy KV rows, tokens held by the running sequences, tokens of KV allocated to them):
+        the occupancy the reference's offline benchmark samples before every step
+        (benchmark/offline_batch_benchmark.cpp:246-266; get_allocated_kv_tokens,
+        scheduler.cpp:700-715)."""
+        used = sum(q.num_prompt + len(q.generated_tokens) for q in self.running)
+        alloc = sum(q.num_blocks for q in self.running) * self.block_size
+        return len(self.running), used, alloc
+
     # ------------------------------------------------------------------ admission, preemption
     def _admit(self) -> None:
         while self.waiting and len(self.running) < self.max_batch:

@@ -658,3 +658,23 @@ def test_native_model_refuses_bad_rows_before_launching(tmp_path):
     assert sum(1 for l in lines if ": " in l and "accepted" not in l) == 8
     calls = [l for l in lines if l.startswith("sq8_")]
     assert len(calls) == 1 and calls[0].startswith("sq8_rope_tables")  # init() only
+
+
+def test_kv_snapshot_equal_in_both_schedulers():
+    """The occupancy snapshot (busy rows, tokens held, tokens allocated) agrees between the two
+    schedulers before every step of a preempting workload."""
+    script, kw = workload(7)
+    snaps = {}
+    for kind in ("python", "native"):
+        model = ChainModel(kw["block_size"])
+        s = (Scheduler if kind == "python" else NativeScheduler)(model, **kw)
+        model.ref = (lambda b: s.alloc.ref[b]) if kind == "python" else s.block_ref
+        for _, ps in script:
+            for p in ps:
+                s.add_request(p)
+        out = []
+        while not s.all_finished() and len(out) < 3000:
+            out.append(s.kv_snapshot())
+            s.step()
+        snaps[kind] = out
+    assert snaps["python"] == snaps["native"] and len(snaps["python"]) > 10
