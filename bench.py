@@ -130,7 +130,24 @@ def cpu_baseline(torch, weights, budget_s=10.0):
         times.append(time.perf_counter() - a)
     rates = sorted(rep_bytes / t / 1e9 for t in times)
     med = float(np.median(rates))
+    # The batched-decode rows too: the same loop at M = 8 and 64 on the same layer, a bounded
+    # sample each (median of at least 3 reps, about budget_s / 4 seconds).
+    sweep = []
+    for M in (8, 64):
+        xm = {p: rng.standard_normal((M, PROJ[p][1]), dtype=np.float32) for p in PROJ}
+        mb = sum(algo_bytes(M, *PROJ[p]) for p in PROJ)
+        mf = sum(2.0 * M * PROJ[p][0] * PROJ[p][1] for p in PROJ)
+        ts, t1 = [], time.perf_counter()
+        while len(ts) < 3 or time.perf_counter() - t1 < budget_s / 4:
+            a = time.perf_counter()
+            for p, q, s in layer:
+                o.matmul_cpu_loop(xm[p], q, s, GS)
+            ts.append(time.perf_counter() - a)
+        tm = float(np.median(ts))
+        sweep.append({"M": M, "GB/s": round(mb / tm / 1e9, 2), "GFLOP/s": round(mf / tm / 1e9, 1),
+                      "reps": len(ts)})
     return {"value": round(med, 2), "unit": "GB/s", "cores": o.max_threads(), "kind": "port",
+            "sweep": sweep,
             "statistic": f"median of {len(times)} reps (min {rates[0]:.1f}, max {rates[-1]:.1f})",
             "sample": "oracle sq8o_matmul_cpu_loop (reference CPU GEMM loop, OpenMP), M=1, one "
                       "rep = one Llama-3-8B layer's qkv, o, gate_up and down projections, "
