@@ -134,3 +134,19 @@ def test_op_library_exports_its_c_interfaces(sq8):
     lib = nat.op_lib()
     for name in declared_functions((sched_h, model_h)):
         assert hasattr(lib, name), name
+
+
+def test_c_headers_compile_as_c(tmp_path):
+    """Every C interface header (include/*.h, the scheduler's and the models') is valid C99, as
+    an FFI host (cgo, a C program) would include it."""
+    import shutil
+    import subprocess
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    inc = REPO / "llm-steadyinfer_amd" / "cpp" / "include"
+    headers = HEADERS + [inc / "scheduler" / "scheduler_c.h", inc / "model" / "batch_model_c.h"]
+    src = tmp_path / "all.c"
+    src.write_text("".join(f'#include "{h}"\n' for h in headers) + "int main(void) { return 0; }\n")
+    res = subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror",
+                          "-fsyntax-only", str(src)], capture_output=True, text=True, timeout=60)
+    assert res.returncode == 0, res.stderr[-3000:]
