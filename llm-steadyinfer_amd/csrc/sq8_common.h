@@ -5,9 +5,10 @@
 
 #include <atomic>
 
+#include "sq8_plan.h"
+
 namespace sq8 {
 
-constexpr int kWave = 64;  // CDNA wavefront width
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));  // 16 int8 weights as one dwordx4
 
@@ -26,28 +27,14 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return (g * sig) * u;
 }
 
-// Weight addressing of the MFMA kernels. A lane of a kernel that feeds v_mfma_f32_16x16x32_f16
-// (or the int8 MFMA) its B operand straight from memory takes, per 64-wide group g, the 16 bytes
-// k = 64 g + 16 (lane / 16) .. +15 of weight row n (n % 16 == lane % 16). Row-major weights
-// ([N][K], the reference's layout) hold them at w + n K + 64 g + 16 (lane / 16): a wave
-// instruction covers 16 rows x 64 B. Packed weights (sq8_pack_weights) store each 16-row tile's
-// group as one 1 KiB block in lane order, tile-major: the same 16 bytes sit at
-// w + (n / 16) 16 K + 1024 g + 16 (16 (lane / 16) + n % 16), so a wave instruction reads 1 KiB
-// contiguously and a tile's K range is one run of 16 K bytes.
-// (The packed address uses the row's own place in its tile, row % 16, so rows whose place differs
-// from the lane's, such as the up rows of a fused gate/up weight with N / 2 % 16 != 0, are read
-// correctly.)
+// Weight addressing of the MFMA kernels: the lane's 16 bytes of group 0 of weight row `row`
+// (ix::lane_woff gives the row-major and packed layouts).
 __device__ __forceinline__ const int8_t* lane_wbase(const int8_t* w, int pk, int row, int K,
                                                     int lane) {
-  return pk ? w + static_cast<size_t>(row >> 4) * K * 16 + ((lane >> 4) * 16 + (row & 15)) * 16
-            : w + static_cast<size_t>(row) * K + (lane >> 4) * 16;
+  return w + ix::lane_woff(pk, row, K, lane);
 }
 // Byte distance between consecutive 64-wide groups of one lane's weights.
-__device__ __forceinline__ int wgroup_step(int pk) { return pk ? 1024 : 64; }
-
-// Bytes of split-K tickets at the start of every MFMA workspace. They must be zero before the
-// first call and every call leaves them zero, so no other use of a workspace may write there.
-constexpr int kWsTicketBytes = 64 * 1024;
+__device__ __forceinline__ int wgroup_step(int pk) { return ix::wgroup_step(pk); }
 
 // Opt a kernel in to `bytes` of dynamic LDS (needed above 64 KiB) once per device: `done` holds
 // one bit per device id below 64 (higher ids set the attribute on every call).

@@ -29,7 +29,6 @@ namespace sq8 {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int BK = 64;          // K per main-loop step = one weight group of 64
 constexpr int LDS_STRIDE = 72;  // halves per staged row (64 + 8 padding against bank conflicts)
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -166,14 +165,8 @@ __device__ __forceinline__ void i8x4_to_h4(uint32_t d, uint32_t& lo, uint32_t& h
 //    threads' loads. The same barrier tells every wave that the stage being refilled next has
 //    been read by all waves. One barrier per 64-wide group.
 // GPS groups per stage: x rows of 8*GPS chunks, w rows of 4*GPS chunks.
-template <int GPS>
-__device__ __forceinline__ int swz_x(int r) {
-  return GPS == 1 ? (r ^ (r >> 3)) & 7 : r & 15;
-}
-template <int GPS>
-__device__ __forceinline__ int swz_w(int r) {
-  return GPS == 1 ? ((r >> 1) ^ (r >> 2)) & 3 : (r ^ (r >> 3)) & 7;
-}
+using ix::swz_w;
+using ix::swz_x;
 
 // One 16-byte global -> LDS copy per lane: lane i writes LDS [lds_base + 16 i]. m0 (the LDS
 // base register of the DMA) is saved and restored around the copy.
@@ -207,58 +200,11 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-template <int WAVES_M, int WAVES_N, int TM, int TN, int STAGES, int GPS>
-struct PTile {
-  static constexpr int NW = WAVES_M * WAVES_N;
-  static constexpr int NT = NW * kWave;
-  static constexpr int BM = WAVES_M * TM * 32;
-  static constexpr int BN = WAVES_N * TN * 32;
-  static constexpr int KB = BK * GPS;            // K per stage
-  static constexpr int CX = 8 * GPS;             // 16-byte chunks per staged x row (hi or lo)
-  static constexpr int CW = 4 * GPS;             // 16-byte chunks per staged weight row
-  static constexpr int XB = BM * CX * 16;        // bytes of x hi (or lo) per stage
-  static constexpr int WB = BN * CW * 16;        // bytes of int8 weights per stage
-  static constexpr int SB = GPS * BN * 8;        // scale bytes per stage (each 32-column run twice)
-  static constexpr int STAGE = 2 * XB + WB + SB;
-  static constexpr size_t LDS_BYTES = static_cast<size_t>(STAGES) * STAGE;
-  static constexpr int XL = BM * CX / NT;        // x DMA instructions per thread per stage (hi or lo)
-  static constexpr int WL = BN * CW / NT;        // weight DMA instructions per thread per stage
-  static constexpr int SL = GPS * BN / 32 / NW;  // scale DMA instructions per thread per stage
-  static constexpr int LOADS = 2 * XL + WL + SL;
-  static_assert(XL >= 1 && WL >= 1 && SL >= 1 && BM * CX % NT == 0 && BN * CW % NT == 0 &&
-                    (GPS * BN / 32) % NW == 0,
-                "tile does not match the DMA pattern");
-  static_assert((STAGES - 2) * LOADS < 64, "vmcnt range");
-  static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
-};
-
-#ifndef SQ8_GEMM_GM
-#define SQ8_GEMM_GM 4
-#endif
-// Output tile (bx, by, bz) of the GEMM's hardware workgroup id. MI355X hands workgroups to its 8
-// XCDs round robin (workgroup b runs on XCD b % 8), and each XCD has its own L2. The grid is
-// renumbered so that each XCD works through one contiguous range of tiles, ordered in bands of
-// GM M-tiles (column by column within a band): the ~32 workgroups an XCD runs at once then
-// share GM activation tiles and 32 / GM weight tiles in its L2, where launch order spread every
-// N-tile over all 8 XCDs and each M-tile over several. A bijection when the grid is a multiple
-// of 8 workgroups; otherwise, and for a single M-tile, the launch order is kept.
+// Output tile (bx, by, bz) of the GEMM's hardware workgroup id: XCD-banded order (ix::gemm_tile).
 __device__ __forceinline__ void gemm_tile_coords(int& bx, int& by, int& bz) {
-  const int X = gridDim.x, Y = gridDim.y, Z = gridDim.z;
-  const int total = X * Y * Z;
-  const int b = blockIdx.x + X * (blockIdx.y + Y * blockIdx.z);
-  bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
-  constexpr int GM = SQ8_GEMM_GM;
-  // A single M-tile (the weight-streaming 64-row tiles) keeps the launch order.
-  if (GM <= 0 || Y == 1 || total % 8 != 0) return;
-  const int L = (b & 7) * (total >> 3) + (b >> 3);
-  const int XY = X * Y;
-  bz = L / XY;
-  const int r = L - bz * XY;
-  const int band = r / (GM * X), row0 = band * GM;
-  const int rows = min(GM, Y - row0);
-  const int q = r - band * GM * X;
-  by = row0 + q % rows;
-  bx = q / rows;
+  const ix::Tile3 t = ix::gemm_tile(blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x, gridDim.y,
+                                    gridDim.z, SQ8_GEMM_GM);
+  bx = t.x, by = t.y, bz = t.z;
 }
 
 template <int WAVES_M, int WAVES_N, int TM, int TN, int STAGES, int GPS>
@@ -286,13 +232,9 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
   // of each output.
   const bool swiglu = epi.mode == kEpiSwiglu;
   const int F = N / 2, f0 = bx * (T::BN / 2);
-  auto feat = [&](int c) __attribute__((always_inline)) {  // SwiGLU feature of tile column c
-    const int tl = c >> 5, jj = (tl % TN) % HT;
-    return f0 + ((tl / TN) * HT + jj) * 32 + (c & 31);
-  };
+  auto feat = [&](int c) __attribute__((always_inline)) { return ix::gemm_feat(c, bx, T::BN, TN); };
   auto wrow = [&](int c) __attribute__((always_inline)) {
-    if (!swiglu) return min(n0 + c, N - 1);
-    return min(feat(c), F - 1) + (((c >> 5) % TN) >= HT ? F : 0);
+    return ix::gemm_row(c, bx, T::BN, TN, N, swiglu);
   };
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem));
 
@@ -310,9 +252,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
     const int r = slot / T::CW, q = (slot % T::CW) ^ swz_w<GPS>(slot / T::CW);
     const uint32_t n = static_cast<uint32_t>(wrow(r));
     // Packed: chunk q of the stage is chunk q % 4 of its group q / 4, in the row's tile block.
-    woff[i] = pk ? (n >> 4) * static_cast<uint32_t>(K) * 16u + (q >> 2) * 1024u +
-                       (((q & 3) * 16u + (n & 15u)) * 16u)
-                 : n * K + q * 16u;
+    woff[i] = ix::gemm_woff(pk, n, K, q);
   }
 #pragma unroll
   for (int i = 0; i < T::SL; ++i) {
@@ -325,7 +265,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
     const char* xhb = reinterpret_cast<const char*>(xh) + static_cast<size_t>(st) * T::KB * 2;
     const char* xlb = reinterpret_cast<const char*>(xl) + static_cast<size_t>(st) * T::KB * 2;
     const char* wb = reinterpret_cast<const char*>(w) +
-                     static_cast<size_t>(st) * (pk ? GPS * 1024 : T::KB);
+                     static_cast<size_t>(st) * ix::gemm_stage_wstep(pk, GPS);
 #pragma unroll
     for (int i = 0; i < T::XL; ++i) {
       const uint32_t d = ((i * T::NW + wave) * kWave) * 16;
@@ -541,11 +481,6 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
   }
 }
 
-// Split-K tickets live at the start of the workspace; each call leaves them zero.
-constexpr int kTicketBytes = kWsTicketBytes;  // ticket array at the start of the workspace
-// K groups per split of the tile kernel: bounds its LDS scale stage (16*T rows x this many).
-constexpr int kTileScaleGroups = 128;
-
 // ---------------------------------------------------------------- skinny decode kernel
 // For 3 <= M <= 64 token rows: one launch, no activation prologue, v_mfma_f32_16x16x32_f16 on
 // MT16 stacked 16-row tiles. A workgroup (4 waves) owns BN = 64*TN output columns, all M rows and
@@ -605,7 +540,7 @@ __global__ __launch_bounds__(kThreads) void skinny16_kernel(
   const float* ssrc[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
-    const int ncol = min(n0 + (wave * TN + j) * 16 + lcol, N - 1);
+    const int ncol = ix::skinny_row(n0, wave, TN, j, lcol, N);
     wsrc[j] = lane_wbase(w, pk, ncol, K, lane) + static_cast<size_t>(gbeg) * gstep;
     ssrc[j] = s + static_cast<size_t>(ncol) * gpr;
   }
@@ -850,7 +785,7 @@ __global__ __launch_bounds__(kThreads) void skinny_i8_kernel(
   const float* ssrc[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
-    const int ncol = min(n0 + (wave * TN + j) * 16 + lcol, N - 1);
+    const int ncol = ix::skinny_row(n0, wave, TN, j, lcol, N);
     wsrc[j] = lane_wbase(w, pk, ncol, K, lane) + static_cast<size_t>(gbeg) * gstep;
     ssrc[j] = s + static_cast<size_t>(ncol) * gpr;
   }
@@ -1170,7 +1105,7 @@ __global__ __launch_bounds__(W * kWave) void tile_kernel(
   const int8_t* wrow[T];
 #pragma unroll
   for (int j = 0; j < T; ++j)
-    wrow[j] = lane_wbase(w, pk, min(n0 + 16 * j + lcol, N - 1), K, lane);
+    wrow[j] = lane_wbase(w, pk, ix::tile_row(n0, j, lcol, N), K, lane);
   const int gstep = wgroup_step(pk);
   const u32x4* xlane = xp + lane;
 
@@ -1379,10 +1314,7 @@ __global__ __launch_bounds__(W * kWave) void dgemm_kernel(
   // Weight row of workgroup column c = (wv * T + j) * 16 + l (SwiGLU: tiles j < T/2 hold the gate
   // rows of the wave's features, tiles j >= T/2 the matching up rows).
   auto wrow = [&](int c) __attribute__((always_inline)) {
-    if (!swiglu) return min(n0 + c, N - 1);
-    const int wv = c / (16 * T), j = (c / 16) % T, l = c % 16;
-    const int f = f0 + (wv * HT + j % HT) * 16 + l;
-    return min(f, F - 1) + (j >= HT ? F : 0);
+    return ix::dgemm_row(c, blockIdx.x, T, W, N, swiglu);
   };
   float* sscale = reinterpret_cast<float*>(smem + D * XSTAGE);
   for (int idx = tid; idx < COLS * gcount; idx += W * kWave) {
@@ -1577,124 +1509,7 @@ __global__ __launch_bounds__(kThreads) void epilogue_kernel(const float* __restr
 
 size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 
-// Decode GEMM configuration: 4 waves x 4 column tiles of 16, an 8-deep weight ring, 4 LDS stages.
-constexpr int kDgT = 2, kDgW = 8, kDgDepth = 8;
-// Ring depth for RT row tiles: 4 tiles take 16 KiB of LDS per group, so their ring is shorter.
-constexpr int dg_depth(int rt) { return rt >= 3 ? 4 : kDgDepth; }
-constexpr int kDgCols = 16 * kDgT * kDgW;
-// Groups per split at most: the LDS scale stage holds 256 columns x (64 + 1) floats. At 32 the
-// 64-row Llama LM head (128256 x 4096) was split in two: 290 against 242 us unsplit.
-constexpr int kDgScaleGroups = 64;
-
-// Largest M served by the single-launch skinny kernel.
-constexpr int kSkinnyMaxM = 32;
-
-struct Plan {
-  bool tile;      // pack_x_kernel + tile_kernel (9 <= M <= 64)
-  bool dgemm;     // pack_x_kernel + dgemm_kernel (+ splitk_reduce_kernel); uses rt
-  int rt, tn, tw; // tile: 16-row activation tiles, 16-column tiles per wave, waves per workgroup
-  bool skinny;
-  int kw;         // skinny: K groups per chunk (divides groups_per_split)
-  int cfg;        // GEMM: 1: 64x256 tile, 2: 128x256.  Skinny: 0: MT=1, 1: MT=2
-  int gps;        // GEMM: 64-wide groups per K stage (the split is counted in stages)
-  int bm, bn;
-  int splits;
-  int groups_per_split;
-};
-
-Plan make_plan(int M, int N, int K) {
-  Plan p{};
-  const int nsteps = K / BK;
-  const int target = 2 * cu_count();
-  const int rt = (M + 15) / 16;
-  // Tile kernel for 9..64 tokens, except long rows (K >= 8192) at 16 or fewer tokens (the skinny
-  // kernel is faster there) and at more than 32 tokens (the GEMM is). Configurations from MI355X
-  // sweeps over the Llama-3-8B projections: wide outputs (N >= 16384) take 4 column tiles per
-  // wave and no K split; others take 2 tiles, 8 waves, and split K when the grid has at most
-  // 1024 waves.
-  // Decode GEMM for wide outputs at 33-64 tokens (Llama gate/up at 48 and 64 rows: 59 and 63 us
-  // against 70 and 77 for the tile kernel, which stays ahead on narrower outputs, where the
-  // decode GEMM needs a deep K split to fill the GPU).
-  // 17-32 tokens on wide outputs up to 64Ki columns take it too (Llama gate/up at 24 and 32
-  // rows: 53.4 and 53.7 us against 56.6 and 56.3; the 128256-column LM head stays on the tile
-  // kernel, 209 against 217 us at 24 rows, as do 16 or fewer rows, 47.5 against 50.2).
-  if (M <= 64 && N >= 16384 && (M > 32 || (M > 16 && N <= 65536))) {
-    p.dgemm = true;
-    p.rt = rt;
-    const int tiles = (N + kDgCols - 1) / kDgCols;
-    const int want = std::max(1, (cu_count() + tiles / 2) / tiles);
-    int gpsplit = (nsteps + want - 1) / want;
-    gpsplit = (gpsplit + kDgDepth - 1) / kDgDepth * kDgDepth;
-    p.groups_per_split = std::min(std::min(gpsplit, nsteps), kDgScaleGroups);
-    p.splits = (nsteps + p.groups_per_split - 1) / p.groups_per_split;
-    return p;
-  }
-  if (M > 8 && M <= 64 && !(K >= 8192 && (rt == 1 || rt > 2))) {
-    p.tile = true;
-    p.rt = rt;
-    int splits = 1;
-    if (N >= 16384) {
-      p.tn = 4;
-      p.tw = rt <= 2 ? 4 : 2;
-    } else {
-      p.tn = 2;
-      p.tw = 8;
-      const int waves = ((N + 31) / 32) * p.tw;
-      const int smax = std::max(1, nsteps / p.tw);  // at least one group per wave
-      if (waves <= 1024) splits = std::min(smax, (2048 + waves - 1) / waves);
-    }
-    splits = std::max(splits, (nsteps + kTileScaleGroups - 1) / kTileScaleGroups);
-    p.groups_per_split = (nsteps + splits - 1) / splits;
-    p.splits = (nsteps + p.groups_per_split - 1) / p.groups_per_split;
-    return p;
-  }
-  if (M <= kSkinnyMaxM) {
-    p.skinny = true;
-    p.cfg = 0;
-    p.bm = M <= 8 ? 8 : ((M + 15) / 16) * 16;
-    p.bn = 64;
-    const int blocks = (N + p.bn - 1) / p.bn;
-    const int kw_max = M <= 32 ? 4 : 2;
-    const int target_wg = target;
-    p.kw = 1;
-    while (p.kw < kw_max && nsteps % (2 * p.kw) == 0) p.kw *= 2;
-    const int chunks = nsteps / p.kw;
-    int splits = 1;
-    if (blocks < target_wg && blocks <= kTicketBytes / 4)
-      splits = min(chunks, (target_wg + blocks - 1) / blocks);
-    const int cps = (chunks + splits - 1) / splits;  // chunks per split
-    p.groups_per_split = cps * p.kw;
-    p.splits = (chunks + cps - 1) / cps;
-    return p;
-  }
-  // Pipelined GEMM: one 64 x 256 (M <= 64; 2 stages of 2 groups, 136 KiB of LDS, or 3 stages
-  // of one group when K is an odd number of groups) or 128 x 256 tile (3 stages of one group,
-  // 150 KiB) per workgroup, one workgroup per CU. K is split when that evens out the rounds of
-  // workgroups over the CUs: cost = rounds / splits plus a small charge per split for the
-  // partial tiles and the reduction.
-  p.cfg = M <= 64 ? 1 : 2;
-  // 64-row tiles stream weights: two groups per stage read each weight row 128 bytes (one L2
-  // line) at a time (Llama down projection at 64 rows: 46 against 51 us with one group).
-  p.gps = p.cfg == 1 && K % (2 * BK) == 0 ? 2 : 1;
-  const int nst = nsteps / p.gps;
-  p.bm = M <= 64 ? 64 : 128;
-  p.bn = 256;
-  const int cus = cu_count();
-  const int tiles = ((M + p.bm - 1) / p.bm) * ((N + p.bn - 1) / p.bn);
-  int splits = 1;
-  double best = 1e30;
-  // The 64-row tile streams weights (partials are cheap next to them); the 128-row tile is
-  // MFMA-bound and pays more for its partials.
-  const double charge = p.cfg == 1 ? 0.005 : 0.04;
-  for (int sp = 1; sp <= 16 && sp * 4 <= nsteps; ++sp) {
-    const double rounds = static_cast<double>((tiles * sp + cus - 1) / cus);
-    const double cost = rounds / sp + charge * (sp - 1);
-    if (cost < best - 1e-9) { best = cost; splits = sp; }
-  }
-  p.groups_per_split = (nst + splits - 1) / splits;
-  p.splits = (nst + p.groups_per_split - 1) / p.groups_per_split;
-  return p;
-}
+Plan make_plan(int M, int N, int K) { return make_plan_for(M, N, K, cu_count()); }
 
 template <int WM, int WN, int TM, int TN, int STAGES, int GPS = 1>
 hipError_t launch_gemm(const _Float16* xh, const _Float16* xl, const float* rsc,
@@ -1823,7 +1638,6 @@ hipError_t launch_tile(const float* x, const int8_t* w, const float* s, float* y
 // of a quarter). The four quarters' sums are added with two lane swaps. With S > 1 slices per
 // tile, each unit stores its 16 x MT sums as a partial and takes a ticket; the last unit of the
 // tile sums the S partials in slice order and resets the ticket.
-constexpr int kPgWaves = 8;
 
 template <int MT, int U>
 __global__ __launch_bounds__(kPgWaves * kWave) void pgemv_kernel(
@@ -1837,10 +1651,8 @@ __global__ __launch_bounds__(kPgWaves * kWave) void pgemv_kernel(
   const int lcol = lane & 15, q = lane >> 4;
   const int G = K / BK;
   const int K4 = K / 4;
-  for (int c = tid; c < MT * K4; c += kPgWaves * kWave) {
-    const int m = c / K4, k4 = c - m * K4;
-    xs[c] = *reinterpret_cast<const float4*>(x + static_cast<size_t>(min(m, M - 1)) * K + 4 * k4);
-  }
+  for (int c = tid; c < MT * K4; c += kPgWaves * kWave)
+    xs[c] = *reinterpret_cast<const float4*>(x + ix::pg_xsrc(c, K4, M, K));
   __syncthreads();
 
   const int ntiles = (N + 15) / 16;
@@ -1848,9 +1660,8 @@ __global__ __launch_bounds__(kPgWaves * kWave) void pgemv_kernel(
   for (int u = blockIdx.x * kPgWaves + wave; u < units; u += gridDim.x * kPgWaves) {
     const int tile = u / S, sl = u - tile * S;
     const int g0 = sl * ks, gn = min(ks, G - g0);
-    const int8_t* wb = w + static_cast<size_t>(tile) * K * 16 + static_cast<size_t>(g0) * 1024 +
-                       lane * 16;
-    const float* sr = s + static_cast<size_t>(min(tile * 16 + lcol, N - 1)) * G + g0;
+    const int8_t* wb = w + ix::pg_wbase(tile, K, g0, lane);
+    const float* sr = s + ix::pg_srow(tile, lcol, N, G, g0);
     float acc[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = 0.f;
@@ -1860,12 +1671,11 @@ __global__ __launch_bounds__(kPgWaves * kWave) void pgemv_kernel(
 #pragma unroll
       for (int v = 0; v < U; ++v)
         wq[v] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(wb + static_cast<size_t>(min(i0 + v, gn - 1)) * 1024));
+            reinterpret_cast<const u32x4*>(wb + static_cast<size_t>(ix::pg_wslot(i0, v, gn)) * 1024));
 #pragma unroll
       for (int v = 0; v < U; v += 4) {
-        // gn % 4 == 0 (K % 256 == 0, ks % 4 == 0): the last whole float4 of the slice is
-        // gn - 4; slots past gn read it again and get scale 0 below.
-        const float4 f = *reinterpret_cast<const float4*>(sr + min(i0 + v, gn - 4));
+        // gn % 4 == 0 (K % 256 == 0, ks % 4 == 0): slots past gn get scale 0 below.
+        const float4 f = *reinterpret_cast<const float4*>(sr + ix::pg_sslot(i0, v, gn));
         sc[v] = f.x;
         sc[v + 1] = f.y;
         sc[v + 2] = f.z;
@@ -1875,7 +1685,7 @@ __global__ __launch_bounds__(kPgWaves * kWave) void pgemv_kernel(
       for (int v = 0; v < U; ++v) {
         __builtin_amdgcn_sched_barrier(0);  // one group's LDS reads at a time
         const i32x4 wv = __builtin_bit_cast(i32x4, wq[v]);
-        const int k4 = (g0 + min(i0 + v, gn - 1)) * 16 + q * 4;
+        const int k4 = (g0 + ix::pg_wslot(i0, v, gn)) * 16 + q * 4;
         const float scv = i0 + v < gn ? sc[v] : 0.f;
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
@@ -1899,7 +1709,7 @@ __global__ __launch_bounds__(kPgWaves * kWave) void pgemv_kernel(
 #pragma unroll
     for (int m = 0; m < MT; ++m)
       if (lane < 16 && m < M && n < N)
-        __hip_atomic_store(part + (static_cast<size_t>(sl) * M + m) * N + n, acc[m],
+        __hip_atomic_store(part + ix::pg_part(sl, M, m, N, n), acc[m],
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // The partial stores are acknowledged before the ticket; the last unit of the tile sums
     // the slices in order.
@@ -1914,7 +1724,7 @@ __global__ __launch_bounds__(kPgWaves * kWave) void pgemv_kernel(
       if (lane < 16 && m < M && n < N) {
         float v = 0.f;
         for (int z = 0; z < S; ++z)
-          v += __hip_atomic_load(part + (static_cast<size_t>(z) * M + m) * N + n,
+          v += __hip_atomic_load(part + ix::pg_part(z, M, m, N, n),
                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         y[static_cast<size_t>(m) * N + n] = v;
       }
@@ -1924,31 +1734,8 @@ __global__ __launch_bounds__(kPgWaves * kWave) void pgemv_kernel(
   }
 }
 
-#ifndef SQ8_PGEMV_U
-#define SQ8_PGEMV_U 4
-#endif
-#ifndef SQ8_PGEMV_WPC
-#define SQ8_PGEMV_WPC 2
-#endif
-struct PgPlan {
-  int ks, S, grid;
-  size_t lds;
-};
 PgPlan pgemv_plan(int M, int N, int K) {
-  PgPlan p{};
-  const int G = K / BK, ntiles = (N + 15) / 16;
-  p.lds = static_cast<size_t>(M) * K * sizeof(float);
-  const int wgs = p.lds > 80 * 1024 ? 1 : SQ8_PGEMV_WPC;  // resident workgroups per CU
-  p.grid = cu_count() * wgs;
-  const int slots = p.grid * kPgWaves;
-  int S = std::max(1, (slots + ntiles - 1) / ntiles);
-  if (ntiles > kTicketBytes / 4) S = 1;
-  int ks = (G + S - 1) / S;
-  ks = std::max(4, (ks + 3) / 4 * 4);  // whole float4s of scales
-  p.ks = ks;
-  p.S = (G + ks - 1) / ks;
-  p.grid = std::min(p.grid, (ntiles * p.S + kPgWaves - 1) / kPgWaves);
-  return p;
+  return pgemv_plan_for(M, N, K, cu_count(), SQ8_PGEMV_WPC);
 }
 
 template <int MT>
@@ -1969,17 +1756,8 @@ hipError_t launch_pgemv_mt(const float* x, const int8_t* w, const float* s, floa
   return hipGetLastError();
 }
 
-#ifndef SQ8_PGEMV_MAX_M
-#define SQ8_PGEMV_MAX_M 2
-#endif
-// Token rows up to which packed weights take the GEMV (above, the int8-limb MFMA kernel).
-constexpr int kPgMaxM = SQ8_PGEMV_MAX_M;
-
-// Packed weights at 1-2 token rows with group size 64 and whole float4s of scales per row.
 bool pgemv_ok(int M, int K, int gs, const float* s) {
-  return M <= kPgMaxM && gs == BK && K % (4 * BK) == 0 &&
-         (reinterpret_cast<uintptr_t>(s) & 15) == 0 &&
-         static_cast<size_t>(M) * K * sizeof(float) <= 144 * 1024;
+  return pgemv_ok_for(M, K, gs, (reinterpret_cast<uintptr_t>(s) & 15) == 0);
 }
 
 hipError_t launch_pgemv(const float* x, const int8_t* w, const float* s, float* y, void* ws,
