@@ -178,8 +178,11 @@ bool Scheduler::ensure_blocks_for(Sequence* seq, int position, const std::vector
 std::vector<Scheduler::BatchRow> Scheduler::build_batch_rows() {
   std::vector<BatchRow> rows;
   std::vector<int> in_rows;  // sequences holding a row of this step: never victims
-  for (size_t i = 0; i < running_.size(); ++i) {
-    Sequence* s = running_[i];
+  // Both passes walk a snapshot: a preemption inside ensure_blocks_for rebuilds running_ without
+  // its victims, and a walk by index over the new list would skip the sequence after one. A
+  // preempted entry of the snapshot fails the state check.
+  const std::vector<Sequence*> snap = running_;
+  for (Sequence* s : snap) {
     if (s->state != SeqState::RUNNING || s->is_finished || !s->is_prefill_complete) continue;
     if (static_cast<int>(rows.size()) >= max_batch_size_) break;
     const int pos = s->num_prompt_tokens + static_cast<int>(s->generated_tokens.size()) - 1;
@@ -212,8 +215,8 @@ std::vector<Scheduler::BatchRow> Scheduler::build_batch_rows() {
   prefill_token_budget_ = std::max(512, std::min(4096, prefill_token_budget_));
 
   int taken = 0;
-  for (size_t i = 0; i < running_.size(); ++i) {
-    Sequence* s = running_[i];
+  const std::vector<Sequence*> snap2 = running_;
+  for (Sequence* s : snap2) {
     if (s->state != SeqState::RUNNING || s->is_finished || s->is_prefill_complete) continue;
     if (taken >= prefill_token_budget_ || static_cast<int>(rows.size()) >= max_batch_size_)
       break;

@@ -109,6 +109,28 @@ def test_native_equals_python_step_for_step(seed):
     assert nat[3].invariant_holds()
 
 
+# A preemption inside the decode pass removes a prefill-incomplete victim that sits before the
+# sequence being grown; the native scheduler once walked its running list by index after that
+# list was rebuilt, so the sequence after the grown one lost its row for the step (this workload
+# diverged from the Python scheduler at step 16 before the walk used a snapshot).
+_EARLIER_VICTIM = (
+    [(2, [[2631, 3399]]), (3, [[416, 216, 4989]]), (4, [[3126, 1574, 1094, 4025]]),
+     (6, [[1132, 2054, 1253, 1919]]),
+     (6, [[807, 3566, 3218, 3872, 4561, 4647, 4973, 4354, 4847, 4690]])],
+    dict(max_batch=4, max_seq_len=28, max_gen_len=18, block_size=4, num_blocks=5,
+         prefix_cache=False, stop_tokens=set()))
+
+
+def test_native_keeps_rows_after_an_earlier_victim_is_preempted():
+    script, kw = _EARLIER_VICTIM
+    py = drive("python", script, max_steps=400, **kw)
+    nat = drive("native", script, max_steps=400, **kw)
+    assert py[2][2] > 0, "the workload must preempt"
+    assert nat[0] == py[0]
+    assert nat[1] == py[1] and nat[2] == py[2]
+    assert nat[3].invariant_holds()
+
+
 def test_native_workloads_exercise_every_mechanism():
     """Across the seeds above, preemption, prefix sharing and stop tokens all occur."""
     pre = shared = stopped = 0
