@@ -251,7 +251,7 @@ __device__ __forceinline__ float row16_sum(float v) {
 // n_target + rows of them per kv head; blockIdx.x / kv_head_num picks a work item (items numbered
 // row by row) and a workgroup past the last item exits at once. A row of one chunk writes its
 // output directly. Otherwise each chunk stores its un-normalised head outputs, max and sum to
-// part (agent-scope stores, acknowledged before the ticket), takes a ticket per (row, kv head),
+// part (agent-scope stores, released before the ticket), takes a ticket per (row, kv head),
 // and the chunk that finishes last merges the row's chunks and resets the ticket to zero.
 template <int DPL, int GMAX, int W>
 __global__ __launch_bounds__(W * kWave) void paged_attention_rows_kernel(
@@ -475,9 +475,7 @@ __global__ __launch_bounds__(W * kWave) void paged_attention_rows_kernel(
     }
   }
   if (nchunks == 1) return;
-  // Wait until this thread's partial stores are acknowledged (s_waitcnt with every counter at
-  // zero) before the workgroup takes its ticket.
-  __builtin_amdgcn_s_waitcnt(0);
+  publish_partials();
   __shared__ bool is_last;
   __syncthreads();
   if (threadIdx.x == 0)
@@ -486,6 +484,7 @@ __global__ __launch_bounds__(W * kWave) void paged_attention_rows_kernel(
               static_cast<unsigned>(nchunks - 1);
   __syncthreads();
   if (!is_last) return;
+  acquire_partials();
   // Merge in batches of kMergeBatch chunks, every load of a batch issued before any is used (one
   // memory latency per batch, not per chunk), with a running max across batches.
   constexpr int kMergeBatch = 8;

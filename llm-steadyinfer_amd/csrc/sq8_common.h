@@ -36,6 +36,18 @@ __device__ __forceinline__ const int8_t* lane_wbase(const int8_t* w, int pk, int
 // Byte distance between consecutive 64-wide groups of one lane's weights.
 __device__ __forceinline__ int wgroup_step(int pk) { return ix::wgroup_step(pk); }
 
+// Hand-off of partial results between workgroups (split-K and split-KV reductions): every thread
+// that stored partials runs publish_partials() before its workgroup (or wave) takes a ticket, and
+// the taker of the last ticket runs acquire_partials() before reading them. The agent-scope
+// release and acquire fences order the partial stores before the ticket and the loads after it
+// for the compiler and the memory system alike (each XCD has its own L2).
+__device__ __forceinline__ void publish_partials() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+}
+__device__ __forceinline__ void acquire_partials() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
 // Opt a kernel in to `bytes` of dynamic LDS (needed above 64 KiB) once per device: `done` holds
 // one bit per device id below 64 (higher ids set the attribute on every call).
 inline hipError_t ensure_dynamic_lds(const void* kernel, size_t bytes,

@@ -220,7 +220,7 @@ constexpr int kAttnSplitMinSeq = 512;
 //    is scored from LDS (the cache rows read are 0 .. pos-1, written by earlier steps).
 //  * with a split (sp.chunk > 0) workgroup (head, c) covers positions c*chunk .. +chunk-1 of the
 //    pos + 1 live ones (workgroups past the last live chunk exit at once). Each stores its
-//    un-normalised outputs, max and sum (agent-scope stores, acknowledged before the ticket),
+//    un-normalised outputs, max and sum (agent-scope stores, released before the ticket),
 //    takes a ticket per head, and the last of the head's live chunks merges them in chunk order
 //    and resets the ticket. A single live chunk writes its output directly.
 template <int HS_MAX, bool ROPE>
@@ -407,13 +407,14 @@ __global__ __launch_bounds__(kAttnBlock) void attention_decode_kernel(
       __hip_atomic_store(pp + head_size + 1, lt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  __builtin_amdgcn_s_waitcnt(0);
+  publish_partials();
   __syncthreads();
   if (threadIdx.x == 0)
     s_last = __hip_atomic_fetch_add(sp.tickets + head, 1u, __ATOMIC_RELAXED,
                                     __HIP_MEMORY_SCOPE_AGENT) == static_cast<unsigned>(nlive - 1);
   __syncthreads();
   if (!s_last) return;
+  acquire_partials();
   const float* hp = sp.part + static_cast<size_t>(head) * gridDim.y * sp.stride;
   float gm = -INFINITY;
   for (int ci = 0; ci < nlive; ++ci)
@@ -532,10 +533,11 @@ __global__ __launch_bounds__(kBlock) void argmax_kernel(const float* __restrict_
       }
     __hip_atomic_store(wval + blockIdx.x, bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(widx + blockIdx.x, bidx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);
+    publish_partials();
     last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
            gridDim.x - 1;
     if (last) {
+      acquire_partials();
       float fv = -INFINITY;
       int fi = INT_MAX;
       for (unsigned b = 0; b < gridDim.x; ++b) {

@@ -495,9 +495,9 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * kWave) void gemm_kernel(
 //    dwordx4 per lane per group; a wave instruction covers 16 rows x 64 B);
 //  * A operand for step t in {0,1}: x[m = l%16][(l/16)*16 + 8t .. +8] from LDS (hi, lo);
 //  * result lane l: column l%16, rows 4*(l/16) .. +3.
-// Split-K partials are exchanged with agent-scope relaxed atomic stores and loads (coherent across
-// the XCDs' L2s without a cache writeback); each thread waits for its stores to be acknowledged
-// before the workgroup takes its ticket.
+// Split-K partials are exchanged with agent-scope atomic stores and loads (coherent across the
+// XCDs' L2s), published by a release fence before the workgroup takes its ticket and acquired by
+// the last workgroup before it sums them.
 typedef float f4v __attribute__((ext_vector_type(4)));
 
 template <int MR, int KW, int TN, int MT16, bool F4>
@@ -718,15 +718,14 @@ __global__ __launch_bounds__(kThreads) void skinny16_kernel(
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-  // Wait until this thread's partial stores are acknowledged (s_waitcnt with every counter at
-  // zero) before the workgroup takes its ticket.
-  __builtin_amdgcn_s_waitcnt(0);
+  publish_partials();
   __syncthreads();
   if (tid == 0)
     is_last = __hip_atomic_fetch_add(&tickets[blockIdx.x], 1u, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT) == static_cast<unsigned>(splits - 1);
   __syncthreads();
   if (!is_last) return;
+  acquire_partials();
   const int ncols = min(BN, N - n0);
   for (int idx = tid; idx < M * ncols; idx += kThreads) {
     const int m = idx / ncols, nn = n0 + idx % ncols;
@@ -949,13 +948,14 @@ __global__ __launch_bounds__(kThreads) void skinny_i8_kernel(
         __hip_atomic_store(dst + static_cast<size_t>(m) * N + n, acc[rb][j], __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
-  __builtin_amdgcn_s_waitcnt(0);
+  publish_partials();
   __syncthreads();
   if (tid == 0)
     is_last = __hip_atomic_fetch_add(&tickets[blockIdx.x], 1u, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT) == static_cast<unsigned>(splits - 1);
   __syncthreads();
   if (!is_last) return;
+  acquire_partials();
   const int ncols = min(BN, N - n0);
   for (int idx = tid; idx < M * ncols; idx += kThreads) {
     const int m = idx / ncols, nn = n0 + idx % ncols;
@@ -1247,15 +1247,15 @@ __global__ __launch_bounds__(W * kWave) void tile_kernel(
       __hip_atomic_store(dst + static_cast<size_t>(m) * N + n, out[q] * rscale[m],
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  // Wait until this thread's partial stores are acknowledged before the workgroup takes its
-  // ticket; the last workgroup of the column block sums the splits in order.
-  __builtin_amdgcn_s_waitcnt(0);
+  // The last workgroup of the column block sums the splits in order.
+  publish_partials();
   __syncthreads();
   if (tid == 0)
     is_last = __hip_atomic_fetch_add(&tickets[blockIdx.x], 1u, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT) == static_cast<unsigned>(splits - 1);
   __syncthreads();
   if (!is_last) return;
+  acquire_partials();
   const int ncols = min(16 * T, N - n0);
   for (int idx = tid; idx < M * ncols; idx += NT) {
     const int m = idx / ncols, nn = n0 + idx % ncols;
@@ -1711,14 +1711,14 @@ __global__ __launch_bounds__(kPgWaves * kWave) void pgemv_kernel(
       if (lane < 16 && m < M && n < N)
         __hip_atomic_store(part + ix::pg_part(sl, M, m, N, n), acc[m],
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // The partial stores are acknowledged before the ticket; the last unit of the tile sums
-    // the slices in order.
-    __builtin_amdgcn_s_waitcnt(0);
+    // The last unit of the tile sums the slices in order.
+    publish_partials();
     unsigned t = 0;
     if (lane == 0)
       t = __hip_atomic_fetch_add(&tickets[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     t = __shfl(t, 0, kWave);
     if (t != static_cast<unsigned>(S - 1)) continue;
+    acquire_partials();
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       if (lane < 16 && m < M && n < N) {
