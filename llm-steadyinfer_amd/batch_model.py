@@ -209,9 +209,12 @@ class PagedBatchModel:
         """Capture the decode-only step graphs for the given row counts (default 1..max_rows) up
         front, as a server does at start-up, instead of at the first decode-only step of each
         row count. Each capture follows one eager run on placeholder rows (token 0 at position 0
-        of physical block 0), so call this before any sequence holds cache blocks. Returns the
-        seconds spent."""
+        of physical block 0), which writes K/V into block 0 of every layer: it is refused once a
+        step has run (a sequence may then hold that block). Returns the seconds spent."""
         import time
+        if self.rows_run:
+            raise RuntimeError("capture_decode_graphs after a forward step would overwrite the "
+                               "KV cache of block 0; capture before the first step")
         torch = self.torch
         t0 = time.perf_counter()
         for B in (rows if rows is not None else range(1, self.max_rows + 1)):

@@ -86,8 +86,9 @@ class PagedBatchModel : public scheduler::BatchModel {
                              int32_t* next_tokens) override;
 
   // Captures the decode-only graphs for B = 1 .. max_rows up front, each after one eager run on
-  // placeholder rows (token 0 at position 0 of block 0); call before any sequence holds cache
-  // blocks, as a server does at start-up.
+  // placeholder rows (token 0 at position 0 of block 0), which writes K/V into block 0 of every
+  // layer: an error once forward_batch has run (a sequence may then hold that block). Call it at
+  // start-up, as a server does.
   base::Status capture_decode_graphs();
 
   int64_t graph_replays() const { return graph_replays_; }

@@ -279,6 +279,9 @@ base::Status PagedBatchModel::capture(int B) {
 
 base::Status PagedBatchModel::capture_decode_graphs() {
   if (!ready_) return base::error::InternalError("init() not called");
+  if (rows_run_ > 0)
+    return base::error::InvalidArgument(
+        "capture_decode_graphs after a forward step would overwrite block 0 of the KV cache");
   for (int B = 1; B <= max_rows_; ++B) {
     if (graphs_.count(B)) continue;
     // Placeholder rows: token 0 at position 0 of physical block 0.

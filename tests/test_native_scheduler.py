@@ -495,6 +495,26 @@ def test_native_model_graphs_replay_decode_steps(tmp_path):
     assert g[2] == 1 and g[3] == 1 and g[6] == 1 and g[8] == 1
 
 
+def test_capture_after_a_step_is_refused(tmp_path):
+    """capture_decode_graphs runs placeholder rows that write K/V into block 0: after a step a
+    sequence may hold that block, so both models refuse (C++ with an error, Python raising)."""
+    import subprocess
+    from types import SimpleNamespace
+    steps = _script(np.random.default_rng(3))
+    exe = _calls_exe(tmp_path)
+    B, nd, rows = steps[0]
+    lines = ["batch 0 1 1", f"{B} {nd}", " ".join(str(r[0]) for r in rows),
+             " ".join(str(r[1]) for r in rows), " ".join(str(b) for r in rows for b in r[2]),
+             "capture"]
+    res = subprocess.run([str(exe)], input="\n".join(lines) + "\n", capture_output=True,
+                         text=True, timeout=120)
+    assert res.returncode != 0
+    assert "capture failed: capture_decode_graphs after a forward step" in res.stdout
+    bm = importlib.import_module("llm_steadyinfer_amd.batch_model")
+    with pytest.raises(RuntimeError, match="after a forward step"):
+        bm.PagedBatchModel.capture_decode_graphs(SimpleNamespace(rows_run=3))
+
+
 def _python_decoder_log(prompt, n_new, split):
     import torch
     pkg = load_pkg()
