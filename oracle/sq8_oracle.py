@@ -91,6 +91,20 @@ def make_case(M: int, N: int, K: int, gs: int = 64, seed: int = 1234, w_std: flo
     return x, q, s
 
 
+def elem_err_strict(y, ref):
+    """Element-wise relative error with a floor of 1e-6 * max|ref|: max |y - r| / max(|r|,
+    1e-6 * max|r|). Outputs near zero dominate it: an fp32 sum over K carries an absolute error of
+    order eps * sum |x w|, which next to a 1e-6 * max|r| floor is far above 1e-3 even for the
+    reference kernel's own fp32 order (matmul_refgpu_f32), so it is reported beside rel_errors'
+    figures, not held to their 1e-3 bar."""
+    y = np.asarray(y, np.float64)
+    r = np.asarray(ref, np.float64)
+    amax = float(np.max(np.abs(r))) if r.size else 0.0
+    if amax == 0.0:
+        return float(np.max(np.abs(y))) if y.size else 0.0
+    return float(np.max(np.abs(y - r) / np.maximum(np.abs(r), 1e-6 * amax)))
+
+
 def rel_errors(y, ref):
     """(elementwise, normwise) relative error of y against ref.
 

@@ -5,7 +5,9 @@ fp32 products (oracle sq8o_matmul_f64),
   elementwise  max |y - r| / max(|r|, 1e-3 * max|r|)  <= 1e-3
   normwise     max |y - r| / max|r|                   <= 1e-5
 The reference's own fp32 order (sq8o_matmul_refgpu_f32) sits at about 1e-5 / 1e-7 on the same
-metric (tests/test_oracle.py).
+metric (tests/test_oracle.py). The element-wise figure with a 1e-6 * max|r| floor
+(oracle elem_err_strict) is printed beside them; the reference's own fp32 order reaches 2.6e-3 to
+3.8e-2 on it at the Llama shapes, so it carries no 1e-3 bar.
 """
 import zlib
 
@@ -39,7 +41,8 @@ def run(sq8, dev, x, q, s, gs, offset_bytes=0):
 
 def check(y, ref, label=""):
     elem, norm = o.rel_errors(y, ref)
-    print(f"{label} elem={elem:.3e} norm={norm:.3e}", flush=True)
+    strict = o.elem_err_strict(y, ref)
+    print(f"{label} elem={elem:.3e} norm={norm:.3e} elem_1e-6_floor={strict:.3e}", flush=True)
     assert np.all(np.isfinite(y)), label
     assert elem <= ELEM_TOL and norm <= NORM_TOL, (label, elem, norm)
 

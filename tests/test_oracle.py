@@ -170,3 +170,22 @@ def test_row_subset_equals_full():
     rows = np.array([0, 7, 39])
     sub = o.matmul_f64(x, q[rows].copy(), s.reshape(40, -1)[rows].reshape(-1).copy(), 64)
     np.testing.assert_array_equal(sub, full[:, rows])
+
+
+def test_strict_elementwise_metric():
+    """elem_err_strict floors |r| at 1e-6 * max|r| (the element-wise figure the parity prints
+    carry beside rel_errors'): hand values, then the fact that sets its role: the reference
+    kernel's own fp32 order exceeds 1e-3 on it at a Llama-3-8B shape (outputs near zero)."""
+    r = np.array([[1000.0, 1e-9, -2.0]])
+    y = np.array([[1000.5, 0.0, -2.0]])
+    # floor 1e-3: |0.5|/1000 = 5e-4, |1e-9|/1e-3 = 1e-6, 0
+    assert o.elem_err_strict(y, r) == pytest.approx(5e-4)
+    y2 = np.array([[1000.0, 1e-3, -2.0]])
+    assert o.elem_err_strict(y2, r) == pytest.approx((1e-3 - 1e-9) / 1e-3)
+    assert o.elem_err_strict(np.zeros((1, 2)), np.zeros((1, 2))) == 0.0
+    x, q, s = o.make_case(1, 4096, 4096, 64, seed=7)
+    ref = o.matmul_f64(x, q, s, 64)
+    refgpu = o.matmul_refgpu_f32(x, q, s, 64)
+    strict = o.elem_err_strict(refgpu, ref)
+    elem, norm = o.rel_errors(refgpu, ref)
+    assert strict > 1e-3 > elem and norm < 1e-6
