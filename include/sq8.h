@@ -137,8 +137,9 @@ int sq8_matmul_rmsnorm_rows_packed(float* x, const float* res, const float* norm
  * reference (whose kernel needs no workspace); for callers that cannot allocate device memory
  * (code under graph capture, tight serving loops, harnesses that forbid hipMalloc). The
  * workspace is a fixed device array of SQ8_NOALLOC_SCRATCH_BYTES in the library, one per GPU,
- * held until the process ends; the first call on a device looks up its address and clears its
- * ticket area (a kernel on hip_stream). Shapes whose sq8_workspace_bytes() exceeds it return
+ * held until the process ends; the first call on a device looks up its address (its split-K
+ * tickets start zero and every call leaves them zero, so no call issues a memset or fill, and
+ * calls may be captured into a HIP graph and replayed). Shapes whose sq8_workspace_bytes() exceeds it return
  * SQ8_ERR_WORKSPACE (every Llama-3-8B projection up to 64 token rows fits). All calls on one
  * GPU share the array: calls that overlap in time on one GPU (other streams, other threads)
  * race and must not be issued. Results are bitwise those of sq8_matmul. */

@@ -20,24 +20,17 @@ constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 void* g_ptr[kMaxDevices] = {};  // per device: the address of its copy of `scratch`
 
-__global__ void zero_words_kernel(unsigned* p, int n) {
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
-}
-
-// The current device's scratch address, looked up once per device. The first lookup also
-// clears the split-K ticket area on `st` (every matmul leaves it zero after that), with a fill
-// kernel rather than a memset so that a first call made under graph capture records no memset.
-int scratch_for_current_device(hipStream_t st, void** out) {
+// The current device's scratch address, looked up once per device. The split-K tickets at its
+// start need no clearing: `scratch` has static storage, zero when the code object is loaded on a
+// device, and every matmul leaves its tickets zero. So no call issues a memset or fill, and the
+// first call on a device may be the one made under graph capture.
+int scratch_for_current_device(void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return SQ8_ERR_DEVICE;
   std::lock_guard<std::mutex> lock(g_mu);
   if (!g_ptr[dev]) {
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return SQ8_ERR_DEVICE;
-    const int words = sq8::kWsTicketBytes / 4;
-    hipLaunchKernelGGL(zero_words_kernel, dim3(words / 256), dim3(256), 0, st,
-                       static_cast<unsigned*>(p), words);
-    if (hipGetLastError() != hipSuccess) return SQ8_ERR_LAUNCH;
     g_ptr[dev] = p;
   }
   *out = g_ptr[dev];
@@ -57,9 +50,8 @@ int sq8_matmul_noalloc(const float* x, const int8_t* w, const float* scales, flo
   if (group_size <= 0 || (static_cast<int64_t>(N) * K) % group_size != 0) return SQ8_ERR_GROUP;
   const size_t need = sq8_workspace_bytes(M, N, K, group_size);
   if (need > kScratchBytes) return SQ8_ERR_WORKSPACE;
-  const hipStream_t st = static_cast<hipStream_t>(hip_stream);
   void* ws = nullptr;
-  const int r = scratch_for_current_device(st, &ws);
+  const int r = scratch_for_current_device(&ws);
   if (r != SQ8_OK) return r;
   return sq8_matmul(x, w, scales, y, M, N, K, group_size, ws, kScratchBytes, hip_stream);
 }

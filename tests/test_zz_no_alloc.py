@@ -64,3 +64,35 @@ def test_noalloc_refuses_shapes_beyond_the_scratch(sq8, dev):
     assert _noalloc(sq8, torch, x, q, s, y) == sq8.SQ8_ERR_WORKSPACE
     torch.cuda.synchronize()
     assert bool((y == 7.0).all())  # nothing launched
+
+
+@pytest.mark.gpu
+def test_noalloc_replays_under_graph_capture(sq8, dev):
+    """The entry point for code under graph capture, captured into a HIP graph: each of several
+    replays, with eager work and synchronisation between them, equals the eager sq8_matmul
+    bitwise (split-K tile kernel with tickets, then the decode GEMM with partials)."""
+    import torch
+    for (M, N, K) in ((16, 4096, 4096), (64, 28672, 4096)):
+        x, q, s = _case(torch, dev, M, N, K, seed=3 * M)
+        ref = sq8.matmul(x, q, s, group_size=64)
+        y = torch.full((M, N), float("nan"), device=dev)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):  # one eager call first: the device's scratch lookup
+            assert _noalloc(sq8, torch, x, q, s, y) == sq8.SQ8_OK
+        torch.cuda.current_stream(dev).wait_stream(side)
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), (M, N, K)
+        g = torch.cuda.CUDAGraph()
+        rc = []
+        with torch.cuda.graph(g, stream=side):
+            rc.append(_noalloc(sq8, torch, x, q, s, y))
+        assert rc == [sq8.SQ8_OK]
+        print(f"noalloc graph M={M} N={N} K={K} path={sq8.path_name(M, N, K, 64)}", flush=True)
+        for rep in range(4):
+            y.fill_(float("nan"))
+            sq8.matmul(x[: M // 2], q, s, group_size=64)  # eager work between the replays
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, ref), (M, N, K, rep)
+        del g
