@@ -29,6 +29,14 @@ void add_kernel_hip(const tensor::Tensor& input1, const tensor::Tensor& input2,
                     const tensor::Tensor& output, void* stream);
 
 MatmulKernelQuant get_matmul_kernel_quant8(base::DeviceType device_type);
+
+// As matmul_kernel_hip_qint8 with the weight in the sq8_pack_weights layout (the tensor keeps
+// dims [N, K]; its buffer holds whole 16-row tiles): sq8_matmul_packed. No reference
+// counterpart: MatmulLayer's opt-in packed upload dispatches here.
+void matmul_kernel_hip_qint8_packed(const tensor::Tensor& input, const tensor::Tensor& weight,
+                                    const tensor::Tensor& output, int32_t group_size,
+                                    const tensor::Tensor& scale, const HipConfig* config);
+MatmulKernelQuant get_matmul_kernel_quant8_packed(base::DeviceType device_type);
 AddKernel get_add_kernel(base::DeviceType device_type);
 
 }  // namespace kernel

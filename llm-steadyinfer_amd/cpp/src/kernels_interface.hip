@@ -5,9 +5,13 @@
 
 namespace kernel {
 
-void matmul_kernel_hip_qint8(const tensor::Tensor& input, const tensor::Tensor& weight,
-                             const tensor::Tensor& output, int32_t group_size,
-                             const tensor::Tensor& scale, const HipConfig* config) {
+namespace {
+// Shape checks of the reference's launcher (matmul_kernel.cu:165-185) and one sq8 call on
+// config->stream with the config's workspace.
+template <bool kPacked>
+void matmul_qint8(const tensor::Tensor& input, const tensor::Tensor& weight,
+                  const tensor::Tensor& output, int32_t group_size, const tensor::Tensor& scale,
+                  const HipConfig* config) {
   CHECK(config != nullptr);
   CHECK(!input.is_empty() && input.dims_size() <= 2);
   CHECK(input.device_type() == base::DeviceType::kDeviceHIP);
@@ -22,15 +26,33 @@ void matmul_kernel_hip_qint8(const tensor::Tensor& input, const tensor::Tensor& 
   const int32_t M = in_size / K;
   CHECK_EQ(M, out_size / N);
   auto* cfg = const_cast<HipConfig*>(config);
-  const size_t ws_bytes = sq8_workspace_bytes(M, N, K, group_size);
+  const size_t ws_bytes = kPacked ? sq8_packed_workspace_bytes(M, N, K, group_size)
+                                  : sq8_workspace_bytes(M, N, K, group_size);
   void* ws = cfg->workspace(ws_bytes);
   CHECK(ws_bytes == 0 || ws != nullptr)
       << "sq8_matmul needs a " << ws_bytes << "-byte workspace, which cannot grow while the stream "
       << "captures a graph (HipConfig::reserve_workspace before the capture)";
-  const int rc = sq8_matmul(input.ptr<float>(), weight.ptr<int8_t>(), scale.ptr<float>(),
-                            const_cast<float*>(output.ptr<float>()), M, N, K, group_size, ws,
-                            cfg->workspace_bytes(), cfg->stream);
-  CHECK(rc == SQ8_OK) << "sq8_matmul: " << sq8_status_string(rc);
+  float* y = const_cast<float*>(output.ptr<float>());
+  const int rc =
+      kPacked ? sq8_matmul_packed(input.ptr<float>(), weight.ptr<int8_t>(), scale.ptr<float>(), y,
+                                  M, N, K, group_size, ws, cfg->workspace_bytes(), cfg->stream)
+              : sq8_matmul(input.ptr<float>(), weight.ptr<int8_t>(), scale.ptr<float>(), y, M, N,
+                           K, group_size, ws, cfg->workspace_bytes(), cfg->stream);
+  CHECK(rc == SQ8_OK) << (kPacked ? "sq8_matmul_packed: " : "sq8_matmul: ")
+                      << sq8_status_string(rc);
+}
+}  // namespace
+
+void matmul_kernel_hip_qint8(const tensor::Tensor& input, const tensor::Tensor& weight,
+                             const tensor::Tensor& output, int32_t group_size,
+                             const tensor::Tensor& scale, const HipConfig* config) {
+  matmul_qint8<false>(input, weight, output, group_size, scale, config);
+}
+
+void matmul_kernel_hip_qint8_packed(const tensor::Tensor& input, const tensor::Tensor& weight,
+                                    const tensor::Tensor& output, int32_t group_size,
+                                    const tensor::Tensor& scale, const HipConfig* config) {
+  matmul_qint8<true>(input, weight, output, group_size, scale, config);
 }
 
 namespace {
@@ -56,6 +78,12 @@ void add_kernel_hip(const tensor::Tensor& input1, const tensor::Tensor& input2,
 
 MatmulKernelQuant get_matmul_kernel_quant8(base::DeviceType device_type) {
   if (device_type == base::DeviceType::kDeviceHIP) return matmul_kernel_hip_qint8;
+  LOG_FATAL << "Unknown device type for get an matmul kernel.";
+  return nullptr;
+}
+
+MatmulKernelQuant get_matmul_kernel_quant8_packed(base::DeviceType device_type) {
+  if (device_type == base::DeviceType::kDeviceHIP) return matmul_kernel_hip_qint8_packed;
   LOG_FATAL << "Unknown device type for get an matmul kernel.";
   return nullptr;
 }

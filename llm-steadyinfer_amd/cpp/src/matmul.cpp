@@ -1,6 +1,7 @@
 // MatmulLayer (reference: src/source/op/matmul.cpp:19-195).
 #include "op/matmul.h"
 #include "kernels/kernels_interface.h"
+#include "sq8.h"
 
 namespace op {
 
@@ -67,8 +68,10 @@ base::Status MatmulLayer::forward() {
   output_flat.set_device_type(device_type_);
   if (!is_quant_layer_)
     return base::error::FunctionNotImplement("fp32 weights are served by the reference's GEMM");
-  kernel::get_matmul_kernel_quant8(device_type_)(input_flat, get_weight(0), output_flat,
-                                                 group_size_, scales_, cuda_config_.get());
+  const kernel::MatmulKernelQuant kern =
+      weights_packed_ ? kernel::get_matmul_kernel_quant8_packed(device_type_)
+                      : kernel::get_matmul_kernel_quant8(device_type_);
+  kern(input_flat, get_weight(0), output_flat, group_size_, scales_, cuda_config_.get());
   if (has_bias_) {
     kernel::get_add_kernel(device_type_)(output_flat, get_bias(0), output_flat,
                                          cuda_config_ ? cuda_config_->stream : nullptr);
@@ -110,6 +113,38 @@ void MatmulLayer::to_cuda() {
   hipStream_t st = cuda_config_ ? cuda_config_->stream : nullptr;
   for (auto& b : bias_)
     if (!b.is_empty()) b.to_cuda(st);
+  if (pack_on_upload_ && !weights_packed_) {
+    const base::Status s = pack_weights();
+    CHECK(s) << "packed weight upload: " << s.get_err_msg();
+  }
+}
+
+base::Status MatmulLayer::pack_weights() {
+  if (weights_packed_) return base::error::Success();
+  if (!is_quant_layer_) return base::error::InvalidArgument("packed weights need a quantised layer");
+  const tensor::Tensor& w = get_weight(0);
+  if (w.is_empty() || w.dims_size() != 2 || w.device_type() != base::DeviceType::kDeviceHIP)
+    return base::error::InvalidArgument("packed weights need the [dim0, dim1] weight on the device");
+  const int32_t N = w.get_dim(0), K = w.get_dim(1);
+  if (N != dim0_ || K != dim1_ || K % 64 != 0 || group_size_ <= 0 || group_size_ % 64 != 0 ||
+      K % group_size_ != 0)
+    return base::error::InvalidArgument("packed weights need K % 64 == 0 and a group size that is "
+                                        "a multiple of 64 dividing K");
+  auto alloc = base::HIPDeviceAllocatorFactory::get_instance();
+  auto buf = std::make_shared<base::Buffer>(sq8_packed_weight_bytes(N, K), alloc);
+  if (!buf->ptr()) return base::error::InternalError("packed weight allocation");
+  buf->set_device_type(base::DeviceType::kDeviceHIP);
+  hipStream_t st = cuda_config_ ? cuda_config_->stream : nullptr;
+  const int rc = sq8_pack_weights(w.ptr<int8_t>(), N, K, static_cast<int8_t*>(buf->ptr()), st);
+  if (rc != SQ8_OK) return base::error::InternalError(std::string("sq8_pack_weights: ") +
+                                                      sq8_status_string(rc));
+  // The row-major copy may be released (below) only once the repack has read it.
+  if (hipStreamSynchronize(st) != hipSuccess) return base::error::InternalError("repack");
+  tensor::Tensor packed(base::DataType::kDataTypeInt8, N, K);
+  if (!packed.assign(buf)) return base::error::InternalError("packed weight tensor");
+  weights_[0] = packed;  // dims stay [dim0, dim1]; the buffer holds whole 16-row tiles
+  weights_packed_ = true;
+  return base::error::Success();
 }
 
 }  // namespace op

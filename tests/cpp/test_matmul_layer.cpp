@@ -88,10 +88,20 @@ void test_host() {
   EXPECT(t.index<float>(5) == 5.f && c.index<float>(23) == 23.f, "clone is a deep copy");
   t.reshape({4, 6});
   EXPECT(t.get_dim(1) == 6 && t.index<float>(7) == 7.f, "reshape keeps data");
+  {  // the packed upload refuses what it cannot repack, before any device call
+    auto blob = make_weight_block(32, 128, 64, 3);
+    op::MatmulLayer q(base::DeviceType::kDeviceHIP, 32, 128, true);
+    q.set_group_size(64);
+    STATUS_CHECK(q.set_weight(0, {32, 128}, blob.data(), base::DeviceType::kDeviceCPU));
+    EXPECT(!q.pack_weights() && !q.weights_packed(), "weight still on the host");
+    op::MatmulLayer f(base::DeviceType::kDeviceHIP, 32, 128, false);
+    EXPECT(!f.pack_weights(), "fp32 layer");
+  }
   std::printf("host checks done\n");
 }
 
-void run_case(int M, int N, int K, int gs, bool one_d, bool with_bias) {
+std::vector<float> run_case(int M, int N, int K, int gs, bool one_d, bool with_bias,
+                            bool packed = false) {
   auto blob = make_weight_block(N, K, gs, 100 + M + N);
   Rng r(7 + M);
   std::vector<float> x(static_cast<size_t>(M) * K);
@@ -108,7 +118,9 @@ void run_case(int M, int N, int K, int gs, bool one_d, bool with_bias) {
   int32_t nb = N;
   if (with_bias) STATUS_CHECK(layer.set_bias(0, nb, bias.data(), base::DeviceType::kDeviceCPU));
   layer.set_cuda_config(cfg);
-  layer.to_cuda();  // uploads int8 weights, scales and bias
+  layer.set_packed_weights(packed);
+  layer.to_cuda();  // uploads int8 weights, scales and bias (and repacks the weight if asked)
+  EXPECT(layer.weights_packed() == packed, "packed upload");
 
   auto dev = base::HIPDeviceAllocatorFactory::get_instance();
   tensor::Tensor in = one_d ? tensor::Tensor(base::DataType::kDataTypeFp32, K, true, dev)
@@ -131,10 +143,26 @@ void run_case(int M, int N, int K, int gs, bool one_d, bool with_bias) {
   double norm = 0;
   const double elem = max_rel_err(y, ref, &norm);
   const bool ok = elem <= 1e-3 && norm <= 1e-5;
-  std::printf("%s M=%d N=%d K=%d gs=%d %s%s elem=%.2e norm=%.2e\n", ok ? "PASS" : "FAIL", M, N, K, gs,
-              one_d ? "1-D" : "2-D", with_bias ? " +bias" : "", elem, norm);
+  std::printf("%s M=%d N=%d K=%d gs=%d %s%s%s elem=%.2e norm=%.2e\n", ok ? "PASS" : "FAIL", M, N, K,
+              gs, one_d ? "1-D" : "2-D", with_bias ? " +bias" : "", packed ? " packed" : "", elem,
+              norm);
   std::fflush(stdout);
   if (!ok) ++sq8test::failures();
+  return y;
+}
+
+// The opt-in packed upload against the row-major one: the oracle's tolerance for both, and
+// bit-identical outputs from 3 token rows on (the same kernels with packed addressing).
+void run_packed_pair(int M, int N, int K, bool with_bias) {
+  const std::vector<float> a = run_case(M, N, K, 64, false, with_bias, false);
+  const std::vector<float> b = run_case(M, N, K, 64, false, with_bias, true);
+  if (M >= 3) {
+    const bool same = a.size() == b.size() &&
+                      std::memcmp(a.data(), b.data(), a.size() * sizeof(float)) == 0;
+    std::printf("%s packed == row-major bitwise M=%d N=%d K=%d\n", same ? "PASS" : "FAIL", M, N,
+                K);
+    if (!same) ++sq8test::failures();
+  }
 }
 
 // A workspace that would have to grow while its stream captures a graph is refused (nullptr, no
@@ -169,6 +197,13 @@ void test_gpu() {
   // The workspace is reused across layers of different shapes (zero tickets are preserved).
   run_case(8, 4096, 4096, 64, false, false);
   run_case(8, 28672, 4096, 64, false, false);
+  // Opt-in packed upload (MatmulLayer::set_packed_weights): the packed GEMV at 1-2 rows, the
+  // MFMA kernels with packed addressing from 3 rows on; N not a multiple of 16 pads the last tile.
+  run_packed_pair(1, 4096, 4096, false);
+  run_packed_pair(2, 1000, 1536, true);
+  run_packed_pair(8, 6144, 4096, false);
+  run_packed_pair(32, 4104, 4096, false);
+  run_packed_pair(300, 256, 1024, true);
   test_workspace_refused_while_capturing();
 }
 
