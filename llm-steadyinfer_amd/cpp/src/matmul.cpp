@@ -1,7 +1,7 @@
 // MatmulLayer (reference: src/source/op/matmul.cpp:19-195).
 #include "op/matmul.h"
 #include "kernels/kernels_interface.h"
-#include "sq8.h"
+#include "../../../include/sq8.h"
 
 namespace op {
 

@@ -14,6 +14,7 @@
 // The op layer's kernel table is not used here (no forward runs).
 namespace kernel {
 MatmulKernelQuant get_matmul_kernel_quant8(base::DeviceType) { return nullptr; }
+MatmulKernelQuant get_matmul_kernel_quant8_packed(base::DeviceType) { return nullptr; }
 AddKernel get_add_kernel(base::DeviceType) { return nullptr; }
 }  // namespace kernel
 
