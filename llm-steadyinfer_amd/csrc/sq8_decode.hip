@@ -278,7 +278,11 @@ __global__ __launch_bounds__(kAttnBlock) void attention_decode_kernel(
       }
     }
   };
+  // Both register buffers are requested before the query is staged, so a wave with up to two
+  // chunks (up to 128 unsplit positions) reads the cache in the same memory round trip as the
+  // query, its rotation tables and the token's k and v.
   if (nch > 0) load(0, 0);
+  if (nch > 1) load(1, 1);
 
   if (ROPE) {
     const int half = head_size / 2;
@@ -345,13 +349,14 @@ __global__ __launch_bounds__(kAttnBlock) void attention_decode_kernel(
     for (int i = 0; i < PCH; ++i)
       if (ci * PCH + i < nmine) consume(part[i] * scale, vr[b][i]);
   };
-  // Register double buffer over chunks, the prefetch issued unconditionally (clamped index).
+  // Register double buffer over chunks: a buffer is refilled with the chunk two ahead as soon as
+  // it has been consumed (nch is wave-uniform).
   for (int ci = 0; ci < nch; ci += 2) {
-    load(1, min(ci + 1, nch - 1));
     consume_chunk(0, ci);
+    if (ci + 2 < nch) load(0, ci + 2);
     if (ci + 1 >= nch) break;
-    load(0, min(ci + 2, nch - 1));
     consume_chunk(1, ci + 1);
+    if (ci + 3 < nch) load(1, ci + 3);
   }
   if (ROPE && pos < p1 && wave == (pos - p0) % W) {  // the token's own position, from LDS
     float a = 0.f, v[DPL];
