@@ -518,14 +518,19 @@ def main():
         a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
         b = torch.empty_like(a)
         b.copy_(a)
+        # With --packed, the same calls on packed weights (repacked before the calls; the repack
+        # launches are pack_weights_kernel in the trace).
+        wts = ({p: [(sq8.pack_weights(q), s) for q, s in weights[p][:3]] for p in PROJ}
+               if args.packed else weights)
+        torch.cuda.synchronize()
         for M in (8, 32, 64):
             for p, (N, K) in PROJ.items():
                 x, y = xbuf(M, K), torch.empty((M, N), device=dev)
                 for l in range(3):
-                    Call(sq8, x, *weights[p][l], y, stream, ws)()
+                    Call(sq8, x, *wts[p][l], y, stream, ws)()
                 torch.cuda.synchronize()
         print(json.dumps({"profile_run": "decode_gemm", "M": [8, 32, 64],
-                          "launches_per_shape": 3}))
+                          "launches_per_shape": 3, "packed": bool(args.packed)}))
         return
 
     if args.profile:
