@@ -516,6 +516,13 @@ int replay_all(bool quick) {
           }
         }
       }
+  // packed weights at 1-2 rows whose shape the packed GEMV does not take (K % 256 != 0):
+  // the int8-limb skinny kernel with packed addressing
+  for (int M = 1; M <= 2; ++M)
+    for (int K : {64, 192, 1088, 4160}) {
+      run("skinny", "packed skinny M=" + std::to_string(M) + " K=" + std::to_string(K));
+      for (int N : {1, 17, 1000, 4096}) replay_skinny(M, N, K, 256, 1, none);
+    }
   // other CU counts on the narrower shapes
   for (int cus : {80, 304})
     for (const Shape& s : kShapes) {
