@@ -169,6 +169,26 @@ constexpr size_t pg_xsrc(int c, int K4, int M, int K) {
   return static_cast<size_t>(imin(c / K4, M - 1)) * K + 4 * static_cast<size_t>(c % K4);
 }
 
+// Decode GEMV (sweep_kernel, splitrow_kernel in sq8_gemv.hip): these restate the kernels'
+// expressions for the CPU replay. The kernels keep their own spelling of the same arithmetic
+// (block_row, the step's k and kc, the stage swizzle), which compiles to the code that was
+// measured; routed through these functions, hipcc schedules the sweep differently.
+// A row block b holds R consecutive weight rows, or with `pair` (R = 2, a fused [gate; up] weight
+// of N = 2F rows) gate row b and its up row b + F; rows past N (blocks past the last) read row
+// N - 1 and their sums are dropped.
+constexpr int sw_nblk(int N, int R, bool pair) { return pair ? N / 2 : (N + R - 1) / R; }
+constexpr int sw_row(int b, int r, int R, int N, bool pair) {
+  return pair ? imin(b + r * (N / 2), N - 1) : imin(b * R + r, N - 1);
+}
+// First K byte of lane `lane`'s 16 weights in 1 KiB chunk c of a row (c = st U + u for step st
+// of U chunks); with `tail` (K not a multiple of the step), chunks past K read the row's first
+// 16 bytes and are dropped.
+constexpr int sw_k(int c, int lane) { return c * 1024 + lane * 16; }
+constexpr int sw_kc(int k, int K, bool tail) { return !tail || k < K ? k : 0; }
+// LDS slot of staged float4 number i (bank-conflict swizzle inside each aligned group of 4
+// float4, so a lane's 4 float4 of a 16-element chunk stay in the group).
+constexpr int sw_xslot(int i) { return i ^ ((i >> 4) & 3); }
+
 // Prefill GEMM LDS swizzles (GPS groups per stage: x rows of 8 GPS 16-byte chunks, w rows of
 // 4 GPS): x row r keeps chunk c at slot c ^ swz_x(r), w row r keeps chunk q at slot q ^ swz_w(r).
 template <int GPS>

@@ -1,4 +1,4 @@
-// CPU replay of the address arithmetic of the MFMA and packed-GEMV kernels.
+// CPU replay of the address arithmetic of the GEMV, MFMA and packed-GEMV kernels.
 //
 // The kernels in llm-steadyinfer_amd/csrc/sq8_mfma.hip take their launch plans and every
 // weight/scale/activation/partial index from sq8_plan.h. This program compiles that same header on
@@ -15,11 +15,16 @@
 //  * split-K partial and ticket indices stay in the workspace the library sizes;
 //  * the prefill GEMM's XCD tile order is a bijection and its LDS swizzle loads each staged
 //    chunk once.
-// Two mutations of the index functions must be caught (the replay has teeth): the packed GEMV's
-// scale read without its clamp at 8 groups per step (the over-read that faulted a lab build), and
-// a packed weight address that takes the row's place in its tile from the lane instead of the row.
+// The decode GEMV kernels (sweep, split-row) are replayed the same way for every instantiation the
+// dispatch uses. Mutations of the index functions must be caught (the replay has teeth): the
+// packed GEMV's scale read without its clamp at 8 groups per step (the over-read that faulted a
+// lab build), a packed weight address that takes the row's place in its tile from the lane
+// instead of the row, the GEMV without its tail clamp, and a split row shorter than K.
 // Exit status 0 when every check passes.
+#include <atomic>
 #include <cstdio>
+#include <functional>
+#include <thread>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -27,24 +32,42 @@
 
 #include "sq8_plan.h"
 
+// The split-row GEMV's chunks per wave (SQ8_GEMV_SPLITROW_U in sq8_gemv.hip, and the prologue
+// variant's fixed 5).
+constexpr int SQ8_GEMV_SPLITROW_U_DEFAULT = 5;
+
 using namespace sq8;
 
 namespace {
 
-long g_fail = 0;
-long g_checks = 0;
-std::string g_ctx;
-bool g_quiet = false;  // mutation runs count failures without printing them
+// Per-thread counters (tasks run on a pool of threads); each task's counts are added to the
+// totals when it ends.
+thread_local long g_fail = 0;
+thread_local long g_checks = 0;
+thread_local std::string g_ctx;
+thread_local bool g_quiet = false;  // mutation runs count failures without printing them
+std::atomic<long> g_printed{0};
 
 void fail(const char* what, long long a, long long b) {
   ++g_fail;
-  if (!g_quiet && g_fail <= 20) std::printf("FAIL [%s] %s (%lld, %lld)\n", g_ctx.c_str(), what, a, b);
+  if (!g_quiet && g_printed.fetch_add(1) < 20)
+    std::printf("FAIL [%s] %s (%lld, %lld)\n", g_ctx.c_str(), what, a, b);
 }
 #define CHECK(cond, what, a, b)                                  \
   do {                                                           \
     ++g_checks;                                                  \
     if (!(cond)) fail(what, (long long)(a), (long long)(b));     \
   } while (0)
+
+// The replay as a list of independent tasks, each with the context its failures print.
+struct Task {
+  std::string ctx;
+  std::function<void()> fn;
+};
+std::vector<Task> g_tasks;
+void task(std::string ctx, std::function<void()> fn) {
+  g_tasks.push_back(Task{std::move(ctx), std::move(fn)});
+}
 
 struct Mut {
   bool scale_unclamped = false;  // pgemv: scale float4 at i0 + v instead of min(i0 + v, gn - 4)
@@ -448,6 +471,158 @@ void replay_gemm(int M, int N, int K, int cus, int pk, bool swiglu, const Mut& m
   else replay_gemm_t<2, 4, 2, 2, 3, 1>(M, N, K, p, pk, swiglu, mu);
 }
 
+// ---------------------------------------------------------------- decode GEMV (1-4 rows)
+// sweep_kernel<R, U, MT, GS, TAIL, WV, PRO, PAIR> over a grid of `grid` workgroups: each wave takes
+// row blocks in grid stride and walks the row in steps of U 1 KiB chunks.
+void replay_sweep(int R, int U, int WV, int MT, bool pair, int M, int N, int K, int gs, int cus,
+                  int wpc, bool drop_tail = false) {
+  const bool tail = !drop_tail && K % (1024 * U) != 0;
+  const int nblk = ix::sw_nblk(N, R, pair);
+  const int grid = ix::imin((nblk + WV - 1) / WV, (wpc / WV) * cus);
+  const int GW = grid * WV, gpr = K / gs, nsteps = (K + 1024 * U - 1) / (1024 * U);
+  const int X4 = MT * K / 4;  // staged float4
+  CHECK(grid >= 1, "grid", grid, nblk);
+  CHECK(static_cast<size_t>(MT) * K * 4 <= 128 * 1024, "activation stage", MT * K * 4, 0);
+  // the stage's swizzle is a bijection on the staged float4
+  {
+    std::vector<unsigned char> seen(X4, 0);
+    for (int i = 0; i < X4; ++i) {
+      const int sl = ix::sw_xslot(i);
+      CHECK(sl >= 0 && sl < X4, "stage slot", sl, X4);
+      if (sl >= 0 && sl < X4) ++seen[sl];
+    }
+    long bad = 0;
+    for (unsigned char v : seen) bad += v != 1;
+    CHECK(bad == 0, "stage swizzle is a bijection", bad, X4);
+  }
+  std::vector<unsigned char> cov(static_cast<size_t>(N) * (K / 16), 0);
+  std::vector<unsigned char> out(pair ? N / 2 : static_cast<size_t>(M) * N, 0);
+  for (int gw = 0; gw < GW; ++gw) {
+    int b = gw, st = 0;
+    // the first step's scales are requested before the loop, then one step ahead (clamped rows)
+    auto scales = [&](int bb, int ss) {
+      for (int u = 0; u < U; ++u)
+        for (int lane : {0, 1, 62, 63}) {  // the lanes' K offsets are affine in the lane
+          const int kc = ix::sw_kc(ix::sw_k(ss * U + u, lane), K, tail);
+          for (int r = 0; r < R; ++r) {
+            const size_t at = static_cast<size_t>(ix::sw_row(bb, r, R, N, pair)) * gpr + kc / gs;
+            CHECK(at < static_cast<size_t>(N) * gpr, "GEMV scale read", at, N * gpr);
+          }
+        }
+    };
+    scales(b, 0);
+    while (b < nblk) {
+      for (int u = 0; u < U; ++u)
+        for (int lane = 0; lane < 64; ++lane) {
+          const int k = ix::sw_k(st * U + u, lane);
+          const int kc = ix::sw_kc(k, K, tail);
+          CHECK(kc + 16 <= K, "GEMV weight chunk inside the row", kc, K);
+          for (int r = 0; r < R; ++r) {
+            const int n = ix::sw_row(b, r, R, N, pair);
+            CHECK(n >= 0 && n < N, "GEMV row", n, N);
+            const bool real = pair ? true : b * R + r < N;
+            if (k < K && real) {
+              unsigned char& v = cov[static_cast<size_t>(n) * (K / 16) + kc / 16];
+              if (v < 255) ++v;
+            }
+          }
+          for (int t = 0; t < MT; ++t) {
+            const int i0 = (t * K + kc) / 4;
+            for (int j = 0; j < 4; ++j) {
+              const int slot = i0 + (j ^ ((i0 >> 4) & 3));  // the kernel's read
+              CHECK(slot == ix::sw_xslot(i0 + j) && slot < X4, "x LDS read of float4", slot,
+                    ix::sw_xslot(i0 + j));
+            }
+          }
+        }
+      int b1 = b, st1 = st + 1;
+      if (st1 == nsteps) { st1 = 0; b1 += GW; }
+      scales(b1, st1);
+      if (st == nsteps - 1) {
+        if (pair) {
+          if (b < nblk) ++out[b];
+        } else {
+          for (int r = 0; r < R; ++r)
+            for (int t = 0; t < MT; ++t)
+              if (b * R + r < N && t < M) ++out[static_cast<size_t>(t) * N + b * R + r];
+        }
+      }
+      b = b1;
+      st = st1;
+    }
+  }
+  long bad = 0;
+  for (unsigned char v : cov) bad += v != 1;
+  CHECK(bad == 0, "GEMV reads each 16-byte chunk of each row once", bad, cov.size());
+  bad = 0;
+  for (unsigned char v : out) bad += v != 1;
+  CHECK(bad == 0, "GEMV writes each output once", bad, out.size());
+}
+
+// splitrow_kernel<U, KS, WV>: KS waves per row, wave part p takes chunks p, p + KS, ...
+void replay_splitrow(int U, int KS, int WV, int N, int K, int gs) {
+  const int RW = WV / KS;
+  const int grid = (N + RW - 1) / RW;
+  const bool tail = K != KS * U * 1024;
+  CHECK(K <= KS * U * 1024, "split row covers K", K, KS * U * 1024);
+  std::vector<unsigned char> cov(static_cast<size_t>(N) * (K / 16), 0);
+  for (int bx = 0; bx < grid; ++bx)
+    for (int wave = 0; wave < WV; ++wave) {
+      const int rw = wave / KS, p = wave % KS;
+      const int nr = ix::imin(bx * RW + rw, N - 1);
+      for (int u = 0; u < U; ++u)
+        for (int lane = 0; lane < 64; ++lane) {
+          const int k = ix::sw_k(p + KS * u, lane);
+          const int kc = ix::sw_kc(k, K, tail);
+          CHECK(kc + 16 <= K && kc / gs < K / gs, "split-row chunk inside the row", kc, K);
+          if (k < K && bx * RW + rw < N) {
+            unsigned char& v = cov[static_cast<size_t>(nr) * (K / 16) + kc / 16];
+            if (v < 255) ++v;
+          }
+        }
+    }
+  long bad = 0;
+  for (unsigned char v : cov) bad += v != 1;
+  CHECK(bad == 0, "split-row GEMV reads each chunk once", bad, cov.size());
+}
+
+void replay_gemv_all() {
+  // every sweep_kernel instantiation the dispatch uses (launch_stream, launch_gemv,
+  // launch_gemv_norm_swiglu), on every shape its preconditions allow among these
+  struct Cfg { int R, U, WV, MT, wpc; bool pair; };
+  const Cfg cfgs[] = {
+      {1, 7, 16, 1, 16, false}, {1, 4, 8, 1, 16, false}, {1, 1, 8, 1, 16, false},
+      {1, 2, 8, 1, 16, false},  {2, 1, 4, 1, 16, false}, {2, 2, 4, 1, 16, false},
+      {2, 4, 4, 1, 16, false},  {1, 7, 16, 2, 16, false}, {1, 4, 8, 2, 16, false},
+      {1, 1, 8, 2, 16, false},  {1, 2, 8, 2, 16, false}, {2, 1, 4, 2, 16, false},
+      {2, 2, 4, 2, 16, false},  {2, 4, 4, 2, 16, false}, {1, 4, 8, 4, 16, false},
+      {2, 1, 8, 1, 16, true},   {2, 2, 8, 1, 16, true},  {2, 4, 8, 1, 16, true},
+  };
+  const int Ns[] = {1, 3, 16, 17, 1000, 1536, 2048, 4096, 6144, 17920, 28672, 128256, 151936};
+  const int Ks[] = {64, 256, 1024, 1536, 2048, 4096, 8960, 14336};
+  for (const Cfg& c : cfgs)
+    for (int N : Ns)
+      for (int K : Ks) {
+        if (static_cast<size_t>(c.MT) * K * 4 > (c.MT == 2 ? 128 * 1024 : 64 * 1024)) continue;
+        if (c.pair && N % 2 != 0) continue;
+        if (static_cast<long>(N) * K > 600000000L) continue;
+        // wide shapes: the single-row configurations (the ones the dispatch gives them)
+        if (static_cast<long>(N) * K > 50000000L && (c.MT != 1 || c.U < 4)) continue;
+        for (int M = (c.MT == 4 ? 3 : c.MT); M <= c.MT; ++M) {
+          task("sweep R=" + std::to_string(c.R) + " U=" + std::to_string(c.U) + " WV=" +
+                   std::to_string(c.WV) + " MT=" + std::to_string(c.MT) +
+                   (c.pair ? " pair" : "") + " M=" + std::to_string(M) + " N=" +
+                   std::to_string(N) + " K=" + std::to_string(K),
+               [=] { replay_sweep(c.R, c.U, c.WV, c.MT, c.pair, M, N, K, 64, 256, c.wpc); });
+        }
+      }
+  for (int N : {1, 7, 1536, 2048})
+    for (int K : {8192, 8960, 10240}) {
+      task("splitrow N=" + std::to_string(N) + " K=" + std::to_string(K),
+           [=] { replay_splitrow(SQ8_GEMV_SPLITROW_U_DEFAULT, 2, 16, N, K, 64); });
+    }
+}
+
 struct Shape {
   const char* name;
   int N, K;
@@ -464,13 +639,10 @@ const Shape kShapes[] = {
     {"config 1", 4096, 4096, false},
 };
 
-void run(const char* tag, const std::string& ctx) {
-  (void)tag;
-  g_ctx = ctx;
-}
 
-int replay_all(bool quick) {
+void replay_all(bool quick) {
   const Mut none;
+  replay_gemv_all();
   const int Us[] = {SQ8_PGEMV_U, 8};
   // packed GEMV: every shape at 1 and 2 rows, both step widths
   for (const Shape& s : kShapes)
@@ -480,10 +652,10 @@ int replay_all(bool quick) {
         for (int cus : {256, 80, 304})
           for (int wpc : {1, 2, 4}) {
             if ((big || quick) && (cus != 256 || wpc != SQ8_PGEMV_WPC)) continue;
-            run("pgemv", std::string(s.name) + " pgemv M=" + std::to_string(M) + " U=" +
-                             std::to_string(U) + " cus=" + std::to_string(cus) + " wpc=" +
-                             std::to_string(wpc));
-            replay_pgemv(M, s.N, s.K, cus, wpc, U, none);
+            task(std::string(s.name) + " pgemv M=" + std::to_string(M) + " U=" +
+                     std::to_string(U) + " cus=" + std::to_string(cus) + " wpc=" +
+                     std::to_string(wpc),
+                 [=] { replay_pgemv(M, s.N, s.K, cus, wpc, U, none); });
           }
       }
   // packed GEMV: narrow outputs and short rows
@@ -491,9 +663,9 @@ int replay_all(bool quick) {
     for (int K : {256, 512, 1536, 4096, 14336})
       for (int M = 1; M <= 2; ++M)
         for (int U : Us) {
-          run("pgemv", "pgemv N=" + std::to_string(N) + " K=" + std::to_string(K) + " M=" +
-                           std::to_string(M) + " U=" + std::to_string(U));
-          replay_pgemv(M, N, K, 256, SQ8_PGEMV_WPC, U, none);
+          task("pgemv N=" + std::to_string(N) + " K=" + std::to_string(K) + " M=" +
+                   std::to_string(M) + " U=" + std::to_string(U),
+               [=] { replay_pgemv(M, N, K, 256, SQ8_PGEMV_WPC, U, none); });
         }
   // MFMA kernels, both weight layouts
   const int Ms[] = {3, 4, 5, 8, 9, 12, 16, 17, 24, 32, 33, 40, 48, 64, 65, 100, 128, 256, 2048};
@@ -503,25 +675,23 @@ int replay_all(bool quick) {
         const bool big = static_cast<long>(s.N) * s.K > 200000000L;
         if (quick && big && M != 2048 && M != 64) continue;
         const std::string c = std::string(s.name) + " M=" + std::to_string(M) + (pk ? " packed" : "");
-        run("skinny", c + " skinny");
-        replay_skinny(M, s.N, s.K, 256, pk, none);
-        run("tile", c + " tile");
-        replay_tile(M, s.N, s.K, 256, pk, none);
+        task(c + " skinny", [=] { replay_skinny(M, s.N, s.K, 256, pk, none); });
+        task(c + " tile", [=] { replay_tile(M, s.N, s.K, 256, pk, none); });
         for (int sw = 0; sw <= (s.swiglu ? 1 : 0); ++sw) {
-          run("dgemm", c + " dgemm" + (sw ? " swiglu" : ""));
-          replay_dgemm(M, s.N, s.K, 256, pk, sw, none);
-          if (M >= 64 || !big) {
-            run("gemm", c + " gemm" + (sw ? " swiglu" : ""));
-            replay_gemm(M, s.N, s.K, 256, pk, sw, none);
-          }
+          task(c + " dgemm" + (sw ? " swiglu" : ""),
+               [=] { replay_dgemm(M, s.N, s.K, 256, pk, sw, none); });
+          if (M >= 64 || !big)
+            task(c + " gemm" + (sw ? " swiglu" : ""),
+                 [=] { replay_gemm(M, s.N, s.K, 256, pk, sw, none); });
         }
       }
   // packed weights at 1-2 rows whose shape the packed GEMV does not take (K % 256 != 0):
   // the int8-limb skinny kernel with packed addressing
   for (int M = 1; M <= 2; ++M)
     for (int K : {64, 192, 1088, 4160}) {
-      run("skinny", "packed skinny M=" + std::to_string(M) + " K=" + std::to_string(K));
-      for (int N : {1, 17, 1000, 4096}) replay_skinny(M, N, K, 256, 1, none);
+      task("packed skinny M=" + std::to_string(M) + " K=" + std::to_string(K), [=] {
+        for (int N : {1, 17, 1000, 4096}) replay_skinny(M, N, K, 256, 1, none);
+      });
     }
   // other CU counts on the narrower shapes
   for (int cus : {80, 304})
@@ -529,14 +699,15 @@ int replay_all(bool quick) {
       if (static_cast<long>(s.N) * s.K > 100000000L) continue;
       for (int M : Ms)
         for (int sw = 0; sw <= (s.swiglu ? 1 : 0); ++sw) {
-          run("cus", std::string(s.name) + " M=" + std::to_string(M) + " cus=" + std::to_string(cus));
-          replay_skinny(M, s.N, s.K, cus, 1, none);
-          replay_tile(M, s.N, s.K, cus, 1, none);
-          replay_dgemm(M, s.N, s.K, cus, 1, sw, none);
-          replay_gemm(M, s.N, s.K, cus, 1, sw, none);
+          task(std::string(s.name) + " M=" + std::to_string(M) + " cus=" + std::to_string(cus),
+               [=] {
+                 replay_skinny(M, s.N, s.K, cus, 1, none);
+                 replay_tile(M, s.N, s.K, cus, 1, none);
+                 replay_dgemm(M, s.N, s.K, cus, 1, sw, none);
+                 replay_gemm(M, s.N, s.K, cus, 1, sw, none);
+               });
         }
     }
-  return 0;
 }
 
 // Each mutation must make the replay fail.
@@ -569,6 +740,19 @@ int mutations() {
                 c2);
     if (c1 == 0 || c2 == 0) ++missed;
   }
+  {
+    const long before = g_fail;
+    g_ctx = "mutation: GEMV without its tail clamp";
+    replay_sweep(1, 2, 8, 1, false, 1, 1536, 1536, 64, 256, 16, /*drop_tail=*/true);
+    const long c1 = g_fail - before;
+    g_fail = before;
+    replay_splitrow(4, 2, 16, 1536, 8960, 64);  // 8 KiB of chunks for 8.75 KiB rows
+    const long c2 = g_fail - before;
+    g_fail = before;
+    std::printf("mutation GEMV tail (K=1536, 2 KiB steps): %ld; split row short of K: %ld "
+                "failing checks\n", c1, c2);
+    if (c1 == 0 || c2 == 0) ++missed;
+  }
   g_quiet = false;
   return missed;
 }
@@ -578,8 +762,25 @@ int mutations() {
 int main(int argc, char** argv) {
   const bool quick = argc > 1 && std::strcmp(argv[1], "quick") == 0;
   replay_all(quick);
-  const long real_fail = g_fail;
+  // Largest tasks first, then a pool of threads (the hardware's count, at most 16) pulls them.
+  std::atomic<size_t> next{0};
+  std::atomic<long> fails{0}, checks{0};
+  const unsigned hw = std::thread::hardware_concurrency();
+  const unsigned nt = hw == 0 ? 4 : (hw > 16 ? 16 : hw);
+  std::vector<std::thread> pool;
+  for (unsigned t = 0; t < nt; ++t)
+    pool.emplace_back([&] {
+      for (size_t i = next.fetch_add(1); i < g_tasks.size(); i = next.fetch_add(1)) {
+        g_ctx = g_tasks[i].ctx;
+        g_tasks[i].fn();
+      }
+      fails += g_fail;
+      checks += g_checks;
+    });
+  for (std::thread& t : pool) t.join();
+  const long real_fail = fails.load();
   const int missed = mutations();
-  std::printf("%ld checks, %ld failures, %d mutations missed\n", g_checks, real_fail, missed);
+  std::printf("%zu tasks on %u threads, %ld checks, %ld failures, %d mutations missed\n",
+              g_tasks.size(), nt, checks.load() + g_checks, real_fail, missed);
   return real_fail == 0 && missed == 0 ? 0 : 1;
 }

@@ -22,7 +22,7 @@ def test_kernel_index_replay(tmp_path):
         pytest.skip("g++ not available")
     exe = tmp_path / "test_index_replay"
     src = REPO / "tests" / "cpp" / "test_index_replay.cpp"
-    res = subprocess.run(["g++", "-std=c++17", "-O2", "-Wall", "-Werror", "-I",
+    res = subprocess.run(["g++", "-std=c++17", "-O2", "-Wall", "-Werror", "-pthread", "-I",
                           str(REPO / "llm-steadyinfer_amd" / "csrc"), str(src), "-o", str(exe)],
                          capture_output=True, text=True, timeout=300)
     assert res.returncode == 0, res.stderr[-3000:]
