@@ -592,32 +592,58 @@ def main():
                                         "profiles/ gives the per-kernel durations)",
                 "algo_bytes_per_launch": round(bytes_per_launch)}
 
+    # The sections after the headline metric report an exception as {"error": ...} in their
+    # field (traceback on stderr) instead of losing the whole line.
+    def section(name, fn):
+        try:
+            return fn()
+        except Exception as e:  # noqa: BLE001 - reported in the output line
+            import traceback
+            traceback.print_exc()
+            print(f"# {name} failed: {e!r}", file=sys.stderr, flush=True)
+            return {"error": f"{type(e).__name__}: {e}"}
+
+    def tps(r, key):
+        return r.get(key) if r else None
+
     # ---------------------------------------------------------------- configs 2 and 3 sweep
     sweep = []
-    if not args.no_sweep:
-        for M in (1, 8, 32, 64, 2048):
-            for p, (N, K) in PROJ.items():
-                x, y = xbuf(M, K), torch.empty((M, N), device=dev)
-                reps = LAYERS if M <= 64 else 4
-                cs = [Call(sq8, x, *weights[p][l % LAYERS], y, stream, ws) for l in range(reps)]
-                cs[0]()
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                a.record(stream)
-                for c in cs:
-                    c()
-                b.record(stream)
-                torch.cuda.synchronize()
-                us = a.elapsed_time(b) * 1e3 / reps
-                tflops = cs[0].flops / us / 1e6
-                rec = {"proj": p, "M": M, "N": N, "K": K, "path": sq8.path_name(M, N, K, GS),
-                       "us": round(us, 2), "GB/s": round(cs[0].bytes / us / 1e3, 1),
-                       "TFLOP/s": round(tflops, 2)}
-                if sq8.path_name(M, N, K, GS) == "mfma":
-                    # the f16 MFMA path issues two products (hi and lo) per useful multiply-add
-                    rec["mfma_frac"] = round(2 * tflops / MFMA_F16_PEAK_TFLOPS, 4)
-                sweep.append(rec)
-                del x, y, cs
-            print(f"# sweep M={M} done", file=sys.stderr, flush=True)
+    sweep_error = None
+
+    def run_sweep():
+        if not args.no_sweep:
+            for M in (1, 8, 32, 64, 2048):
+                for p, (N, K) in PROJ.items():
+                    x, y = xbuf(M, K), torch.empty((M, N), device=dev)
+                    reps = LAYERS if M <= 64 else 4
+                    cs = [Call(sq8, x, *weights[p][l % LAYERS], y, stream, ws)
+                          for l in range(reps)]
+                    cs[0]()
+                    a = torch.cuda.Event(enable_timing=True)
+                    b = torch.cuda.Event(enable_timing=True)
+                    a.record(stream)
+                    for c in cs:
+                        c()
+                    b.record(stream)
+                    torch.cuda.synchronize()
+                    us = a.elapsed_time(b) * 1e3 / reps
+                    tflops = cs[0].flops / us / 1e6
+                    rec = {"proj": p, "M": M, "N": N, "K": K, "path": sq8.path_name(M, N, K, GS),
+                           "us": round(us, 2), "GB/s": round(cs[0].bytes / us / 1e3, 1),
+                           "TFLOP/s": round(tflops, 2)}
+                    if sq8.path_name(M, N, K, GS) == "mfma":
+                        # the f16 MFMA path issues two products (hi and lo) per useful multiply-add
+                        rec["mfma_frac"] = round(2 * tflops / MFMA_F16_PEAK_TFLOPS, 4)
+                    sweep.append(rec)
+                    del x, y, cs
+                print(f"# sweep M={M} done", file=sys.stderr, flush=True)
+
+    try:
+        run_sweep()
+    except Exception as e:  # noqa: BLE001 - reported in the output line
+        import traceback
+        traceback.print_exc()
+        sweep_error = f"{type(e).__name__}: {e}"
 
     # Config 3 (prefill, M = 2048): the GEMM is MFMA-bound. Issued f16 MFMA work is twice the
     # useful multiply-adds (hi and lo activation halves); peak = dense f16 MFMA.
@@ -639,9 +665,15 @@ def main():
     # rows of the sweep: 32 back-to-back launches of the shape).
     shape_bytes = [(p, algo_bytes(1, N, K)) for p, (N, K) in PROJ.items()] + \
         [("lm_head", algo_bytes(1, VOCAB, HIDDEN))]
-    rceil = read_ceiling(torch, sq8, dev, shape_bytes) if not args.no_ceiling else None
+    rceil = cceil = None
+    if not args.no_ceiling:
+        ceil = section("ceilings", lambda: (read_ceiling(torch, sq8, dev, shape_bytes),
+                                            copy_ceiling(torch, dev, shape_bytes)))
+        if isinstance(ceil, tuple):
+            rceil, cceil = ceil
+        else:
+            roofline["read_ceiling"] = ceil
     if rceil is not None:
-        cceil = copy_ceiling(torch, dev, shape_bytes)
         gemv_us = {r["proj"]: r["us"] for r in sweep if r["M"] == 1}
         counts = {p: LAYERS for p in PROJ}
         counts["lm_head"] = 1
@@ -665,14 +697,15 @@ def main():
 
     llama = None
     if not args.no_llama_decode:
-        llama = llama_decode_run(torch, weights, lm_head)
-        print(f"# llama decode done: {llama['tokens_per_s']} tokens/s", file=sys.stderr,
+        llama = section("llama decode", lambda: llama_decode_run(torch, weights, lm_head))
+        print(f"# llama decode done: {tps(llama, 'tokens_per_s')} tokens/s", file=sys.stderr,
               flush=True)
 
     decode = None
     if not args.no_decode:
-        decode = decode_run(torch)
-        print(f"# decode done: {decode['tokens_per_s']} tokens/s", file=sys.stderr, flush=True)
+        decode = section("decode", lambda: decode_run(torch))
+        print(f"# decode done: {tps(decode, 'tokens_per_s')} tokens/s", file=sys.stderr,
+              flush=True)
 
     # The same 1-64-row shapes on packed weights (one repack per layer's weight).
     sweep_packed = []
@@ -698,21 +731,22 @@ def main():
 
     batch = None
     if not args.no_batch:
-        batch = batch_run(torch, weights, lm_head, native=args.native_scheduler,
-                          native_model=args.native_model)
-        print(f"# batch done: {batch['output_tokens_per_s']} output tokens/s", file=sys.stderr,
-              flush=True)
+        batch = section("batch", lambda: batch_run(torch, weights, lm_head,
+                                                   native=args.native_scheduler,
+                                                   native_model=args.native_model))
+        print(f"# batch done: {tps(batch, 'output_tokens_per_s')} output tokens/s",
+              file=sys.stderr, flush=True)
     batch_packed = None
     if args.packed and not args.no_batch:
-        batch_packed = batch_run(torch, weights, lm_head, packed=True,
-                                 native=args.native_scheduler,
-                                 native_model=args.native_model)
-        print(f"# packed batch done: {batch_packed['output_tokens_per_s']} output tokens/s",
-              file=sys.stderr, flush=True)
+        batch_packed = section("packed batch", lambda: batch_run(
+            torch, weights, lm_head, packed=True, native=args.native_scheduler,
+            native_model=args.native_model))
+        print(f"# packed batch done: {tps(batch_packed, 'output_tokens_per_s')} output "
+              "tokens/s", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(torch, weights, args.cpu_seconds)
+        cpu = section("cpu baseline", lambda: cpu_baseline(torch, weights, args.cpu_seconds))
 
     out = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
@@ -726,11 +760,11 @@ def main():
         "launch": "hip_graph" if args.graph else "eager",
         "graph_GBps": round(step_bytes / dt_graph / 1e9, 1) if dt_graph else None,
         "decode_matmul_tokens_per_s": round(1.0 / dt, 1),
-        "llama_decode_tokens_per_s": llama["tokens_per_s"] if llama else None,
+        "llama_decode_tokens_per_s": tps(llama, "tokens_per_s"),
         "llama_decode": llama,
-        "decode_tokens_per_s": decode["tokens_per_s"] if decode else None,
+        "decode_tokens_per_s": tps(decode, "tokens_per_s"),
         "decode": decode,
-        "batch_output_tokens_per_s": batch["output_tokens_per_s"] if batch else None,
+        "batch_output_tokens_per_s": tps(batch, "output_tokens_per_s"),
         "batch": batch,
         "batch_packed": batch_packed,
         "step_algo_bytes": step_bytes,
@@ -739,6 +773,7 @@ def main():
         "cpu_baseline": cpu,
         "sweep": sweep,
         "sweep_packed": sweep_packed or None,
+        "sweep_error": sweep_error,
     }
     print(json.dumps(out))
 
