@@ -480,6 +480,9 @@ namespace {
 
 // Launch configurations measured best on MI355X (Llama-3-8B and Qwen2-1.5B decode steps; the
 // values are macros so that variants can be built for A/B runs without editing the dispatch):
+//   NORM_WV         waves per workgroup of the RMSNorm-prologue GEMV with rows of 2-8 KiB (each
+//                   workgroup re-stages the normalised row: fewer, larger workgroups stage it
+//                   fewer times);
 //   LONG_U          KiB per step of rows of 8 KiB and more in 16-wave workgroups, when it divides
 //                   K (Llama down: 7, two steps of 14 KiB rows);
 //   NARROW_WPC      resident waves per CU for N <= 8192 (12, 24 and 32 measured slower);
@@ -490,6 +493,9 @@ namespace {
 //   SPLITROW_*      two waves per row (U chunks of 1 KiB each) in 16-wave workgroups for the plain
 //                   few-long-rows shape (Qwen2 down: 1122 against 1056 tokens/s unsplit; 3 or 4
 //                   waves per row, 8- or 15-wave workgroups, one wave of 9 chunks all slower).
+#ifndef SQ8_GEMV_NORM_WV
+#define SQ8_GEMV_NORM_WV 8
+#endif
 #ifndef SQ8_GEMV_LONG_U
 #define SQ8_GEMV_LONG_U 7
 #endif
@@ -611,6 +617,8 @@ hipError_t launch_stream(const float* x, const int8_t* w, const float* s, float*
     const int wpc = SQ8_GEMV_NARROW_WPC;
     if (u == 1) return launch_sweep<1, 1, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro, wpc);
     if (u == 2) return launch_sweep<1, 2, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro, wpc);
+    if (PRO == kProNorm)  // every workgroup recomputes the norm: workgroup size is a lab knob
+      return launch_sweep<1, 4, SQ8_GEMV_NORM_WV, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro, wpc);
     return launch_sweep<1, 4, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro, wpc);
   }
   if (u == 1) return launch_sweep<2, 1, 4, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
