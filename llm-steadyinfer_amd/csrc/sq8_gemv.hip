@@ -483,8 +483,6 @@ namespace {
 //   NORM_WV         waves per workgroup of the RMSNorm-prologue GEMV with rows of 2-8 KiB (each
 //                   workgroup re-stages the normalised row: fewer, larger workgroups stage it
 //                   fewer times);
-//   LONG_U          KiB per step of rows of 8 KiB and more in 16-wave workgroups, when it divides
-//                   K (Llama down: 7, two steps of 14 KiB rows);
 //   NARROW_WPC      resident waves per CU for N <= 8192 (12, 24 and 32 measured slower);
 //   PAIR_WV, _WPC   the row-pair (gate/up + SwiGLU) GEMV: 8-wave workgroups, 16 waves per CU
 //                   (4-wave: 22.6 -> 23.7 us on Llama gate/up; 7 waves: 35 us; 24-32 per CU slower);
@@ -495,9 +493,6 @@ namespace {
 //                   waves per row, 8- or 15-wave workgroups, one wave of 9 chunks all slower).
 #ifndef SQ8_GEMV_NORM_WV
 #define SQ8_GEMV_NORM_WV 8
-#endif
-#ifndef SQ8_GEMV_LONG_U
-#define SQ8_GEMV_LONG_U 7
 #endif
 #ifndef SQ8_GEMV_NARROW_WPC
 #define SQ8_GEMV_NARROW_WPC 16
@@ -608,8 +603,7 @@ hipError_t launch_stream(const float* x, const int8_t* w, const float* s, float*
         x, w, s, y, N, K, gs, st, pro);
 #endif
   if (K >= 8192) {
-    return K % (1024 * SQ8_GEMV_LONG_U) == 0
-               ? launch_sweep<1, SQ8_GEMV_LONG_U, 16, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro)
+    return K % 7168 == 0 ? launch_sweep<1, 7, 16, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro)
                          : launch_sweep<1, 4, 8, MT, PRO>(x, w, s, y, M, N, K, gs, st, pro);
   }
   const int u = K <= 1024 ? 1 : (K <= 2048 ? 2 : 4);
